@@ -1,0 +1,249 @@
+"""Benchmark of the MI355X embedding lookup path (one JSON line on stdout).
+
+Default workload (BASELINE.json's metric, C2-pool): GPUEmbeddingLayer over a
+50,000,000 x 128 fp16 table in HBM (values N(0, 0.02)), 262,144 int64 keys per
+batch drawn Zipf(alpha=1.05) over the rows with a seeded permutation (the
+reference's generator, samples/pytorch/pytorch_samples_common.py:21-47),
+fused find-and-pool with Fixed hotness 1024 x 256 bags, Sum, fp16 output,
+through the C ABI entry nve_layer_lookup_pooled.  A step is one lookup of one
+batch; batches are generated up front and stay resident in HBM.
+
+Reported beside the throughput:
+  roofline      algorithmic bytes per launch / the kernel's mean duration
+                (HIP events on the lookup stream) against the 8 TB/s HBM peak,
+                and against the measured random-row read ceiling;
+  cpu_baseline  the reference HostLayer algorithm (threaded gather + fp32
+                pooling, oracle/ restatement) timed on this host's cores on a
+                bounded sample of the same batches.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "nv-embedding-cache_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "embedding lookups/sec + achieved HBM GB/s (% peak), fused find-and-pool, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def power_law_keys(torch, n, rows, alpha, gen, perm):
+    """translateToPowerLaw(1, rows, alpha, x) then perm[y] (pytorch_samples_common.py:21-47)."""
+    x = torch.rand(n, device="cuda", dtype=torch.float64, generator=gen)
+    gamma = torch.tensor([1.0 - alpha], device="cuda")  # float32, as the reference
+    lo = torch.pow(torch.tensor(1.0, device="cuda"), gamma)
+    hi = torch.pow(torch.tensor(float(rows), device="cuda"), gamma)
+    y = torch.pow(x * (hi - lo) + lo, 1.0 / gamma)
+    y[y >= rows] = rows - 1
+    return perm[y.to(torch.int64)]
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, avail
+
+
+def cpu_baseline(torch, d_table, key_batches, bags, hot, rows, dim, seconds):
+    """HostLayer restatement (oracle/, the checker library) timed on host cores."""
+    import numpy as np
+    from oracle import oracle as O
+
+    model, avail = cpu_info()
+    threads = max(avail - 2, 1)  # SimpleThreadPool default (thread_pool.cpp:112-116)
+    log(f"cpu baseline: copying the table to host ({rows} x {dim} fp16)")
+    h_table = d_table.view(torch.int16).cpu().numpy().view(np.uint8).reshape(-1)
+    keys = [k.cpu().numpy() for k in key_batches]
+    # one warm-up batch, then whole batches until `seconds` of work
+    O.host_layer_lookup(keys[0], h_table, rows, dim * 2, O.F16, O.SUM, O.FIXED, None, bags, hot,
+                        None, 0, O.F16, threads)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        O.host_layer_lookup(keys[done % len(keys)], h_table, rows, dim * 2, O.F16, O.SUM, O.FIXED,
+                            None, bags, hot, None, 0, O.F16, threads)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and done >= 3:
+            break
+    n = keys[0].size
+    return {"value": done * n / el, "unit": "lookups/s", "cores": threads, "kind": "port",
+            "sample": f"{done} full batches of {n} keys (Fixed {hot} x {bags} bags, Sum, fp16) "
+                      f"in {el:.1f} s on '{model}' ({avail} cores available, {threads} worker threads)"}
+
+
+def read_ceiling(torch, lib, stream, seconds_cap=2.0):
+    """Random-row read ceiling: uniform random 256-byte rows from a 16 GiB buffer."""
+    row_bytes = 256
+    rows = (16 << 30) // row_bytes
+    buf = torch.empty(rows * row_bytes // 2, dtype=torch.int16, device="cuda")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    n = 262144 * 4
+    idx = torch.randint(0, rows, (n,), device="cuda", generator=gen, dtype=torch.int64)
+    sink = torch.zeros((n + 127) // 128, dtype=torch.int32, device="cuda")
+    s = ctypes.c_void_p(stream.cuda_stream)
+
+    def launch():
+        lib.call("nve_amd_read_ceiling", ctypes.c_void_p(buf.data_ptr()), row_bytes,
+                 ctypes.c_void_p(idx.data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
+
+    for _ in range(5):
+        launch()
+    reps = 50
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del buf
+    torch.cuda.empty_cache()
+    return (n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rows", type=int, default=50_000_000)
+    ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--bags", type=int, default=256)
+    ap.add_argument("--hotness", type=int, default=1024)
+    ap.add_argument("--alpha", type=float, default=1.05)
+    ap.add_argument("--batches", type=int, default=16, help="distinct key batches cycled")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the lookup path is single-GPU; "
+              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from pynve import _lib
+
+    lib = _lib
+    _lib.load()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    rows, dim, bags, hot = args.rows, args.dim, args.bags, args.hotness
+    nkeys = bags * hot
+    width = dim * 2
+
+    log(f"table {rows} x {dim} fp16 ({rows * width / 1e9:.1f} GB), {nkeys} keys/batch")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    d_table = torch.empty((rows, dim), dtype=torch.float16, device="cuda")
+    chunk = 1 << 24
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        d_table[r0:r1].normal_(0.0, 0.02, generator=gen)
+    pgen = torch.Generator(device="cuda")
+    pgen.manual_seed(31337)
+    perm = torch.randperm(rows, generator=pgen, device="cuda", dtype=torch.int64)
+    kgen = torch.Generator(device="cuda")
+    kgen.manual_seed(1)
+    batches = [power_law_keys(torch, nkeys, rows, args.alpha, kgen, perm) for _ in range(args.batches)]
+    del perm
+    out = torch.empty((bags, dim), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    uniq = torch.unique(batches[0]).numel()
+    log(f"keys ready: {uniq} unique in batch 0 ({100.0 * uniq / nkeys:.1f} %)")
+
+    stream = torch.cuda.Stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    L = _lib.load()
+    cfg = L.nve_gpu_embedding_layer_config_default()
+    cfg.layer_name = b"bench"
+    cfg.embedding_table = d_table.data_ptr()
+    cfg.num_embeddings = rows
+    cfg.embedding_width_in_bytes = width
+    cfg.value_dtype = _lib.DT_F16
+    layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
+    _lib.call("nve_gpu_embedding_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(cfg), None)
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
+    look = L.nve_layer_lookup_pooled
+    kptrs = [ctypes.c_void_p(b.data_ptr()) for b in batches]
+    optr = ctypes.c_void_p(out.data_ptr())
+
+    def step(i):
+        st = look(layer, ctx, nkeys, kptrs[i % len(kptrs)], optr, width, None, _lib.POOL_SUM,
+                  _lib.SPARSE_FIXED, None, 0, hot, None, _lib.DT_UNKNOWN, _lib.DT_F16, None)
+        if st:
+            _lib.check(st)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    log(f"timed {args.steps} steps: {ms * 1000:.2f} us/step (events), wall {wall * 1e3 / args.steps * 1000:.2f} us/step")
+
+    # algorithmic bytes per launch: keys + one stored row per key + pooled output
+    alg = nkeys * 8 + nkeys * width + bags * width
+    achieved = alg / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "kernel": "pool_kernel<F16,16>", "alg_bytes_per_launch": alg}
+    tf = os.path.join(ROOT, "profiles", "c2pool_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            roof["traffic"] = json.load(f).get("traffic_bytes_per_launch")
+    result = {"metric": METRIC, "value": round(nkeys / (ms * 1e-3), 1), "unit": "lookups/s",
+              "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+              "data": "synthetic",
+              "config": {"workload": "C2-pool: GPUEmbeddingLayer fused find-and-pool, fp16 table in HBM",
+                         "table_rows": rows, "dim": dim, "row_dtype": "f16", "keys_per_batch": nkeys,
+                         "zipf_alpha": args.alpha, "bags": bags, "hotness": hot, "pooling": "sum",
+                         "output_dtype": "f16", "accumulate": "f32", "key_batches_cycled": args.batches},
+              "roofline": roof}
+    if not args.no_ceiling:
+        ceil, cms = read_ceiling(torch, _lib, stream)
+        log(f"random-row read ceiling: {ceil:.0f} GB/s ({cms * 1000:.1f} us per 1M rows)")
+        result["ceiling"] = {"random_row_read_GBps": round(ceil, 1),
+                             "frac_of_ceiling": round(achieved / ceil, 4)}
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(torch, d_table, batches[:4], bags, hot, rows, dim,
+                                              args.cpu_seconds)
+        result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 1)
+    _lib.call("nve_context_wait", ctx)
+    _lib.call("nve_context_destroy", ctx)
+    _lib.call("nve_layer_destroy", layer)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,70 @@
+/*
+ * nve_amd_ext.h -- extensions of the MI355X lookup library beyond the
+ * reference's C ABI (include/nve_c_api.h).  Same conventions: every call
+ * returns nve_status_t, messages go to nve_get_last_error, streams are
+ * hipStream_t passed as void*.  Pointers documented as "device" must be
+ * GPU-readable (device memory, or pinned host memory for a table).
+ */
+#ifndef NVE_AMD_EXT_H
+#define NVE_AMD_EXT_H
+
+#include "nve_c_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Row formats without a reference counterpart (the reference has no int8
+ * affine row with fp32 offset and no fp8 row; nve_types.hpp:59-73).  Both
+ * dequantize in fp32 and may be emitted as fp16 or fp32:
+ *   NVE_DTYPE_X_INT8_AFFINE_F32: int8 q[count], f32 scale, f32 offset;
+ *                                value = fma(q, scale, offset)
+ *   NVE_DTYPE_X_E4M3_ROWWISE_F32: OCP fp8 e4m3 q[count], f32 scale;
+ *                                value = e4m3(q) * scale */
+enum {
+  NVE_DTYPE_X_INT8_AFFINE_F32 = 32,
+  NVE_DTYPE_X_E4M3_ROWWISE_F32 = 33,
+};
+
+/* Fused find-and-pool over a linear table, keys and outputs in device memory.
+ * Restates the reference's kernel-level router find_and_pool
+ * (cuda_ops/find_and_pool.cuh:103-132) with a linear table
+ * (ECNoCache, load_indices = true): Concatenate emits one dequantized row per
+ * key, every other pooling type one fp32-accumulated row per bag.
+ * output_type: the value type's float precision (either precision for the
+ * extension types).  split_hint: 0 lets the library choose how many lane
+ * groups share a bag; > 0 forces that many (a power of two); < 0 forces one
+ * group per bag (strict key order). */
+NVE_C_API nve_status_t nve_amd_find_and_pool(
+    nve_key_type_t key_type, int64_t num_keys, const void* keys, const void* table,
+    int64_t num_rows, int64_t row_size_in_bytes, nve_data_type_t value_dtype,
+    nve_pooling_type_t pooling_type, nve_sparse_type_t sparse_type, const void* csr_offsets,
+    int64_t num_csr_offsets, int64_t fixed_hotness, const void* weights,
+    nve_data_type_t weight_type, nve_data_type_t output_type, void* output,
+    int64_t output_stride, int32_t split_hint, void* stream);
+
+/* Random-row read ceiling microbenchmark: reads row idx[i] (row_size_in_bytes
+ * each, a multiple of 16) of a device table for i < n and folds the bytes into
+ * sink (one uint32 per 256-thread workgroup, ceil(n/128) words). */
+NVE_C_API nve_status_t nve_amd_read_ceiling(const void* table, int64_t row_size_in_bytes,
+                                            const int64_t* idx, int64_t n, uint32_t* sink,
+                                            void* stream);
+
+/* Cache state transfer of a GPU table (checkpoint-style restore, tests):
+ * tags = num_sets*8 keys of the table's key type, counters = num_sets*8
+ * float, set_ts = num_sets int64; host or device pointers; any may be NULL. */
+NVE_C_API nve_status_t nve_amd_gpu_table_num_sets(const nve_table_t table, int64_t* out);
+NVE_C_API nve_status_t nve_amd_gpu_table_export_state(nve_table_t table, void* tags,
+                                                      float* counters, int64_t* set_ts,
+                                                      int64_t* global_ts);
+NVE_C_API nve_status_t nve_amd_gpu_table_import_state(nve_table_t table, const void* tags,
+                                                      const float* counters,
+                                                      const int64_t* set_ts, int64_t global_ts);
+/* Device address of the cache rows ((set*8 + way) * row_size_in_bytes). */
+NVE_C_API nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVE_AMD_EXT_H */

@@ -1,0 +1,331 @@
+// device_common.cuh -- device helpers shared by the lookup kernels (gfx950, wave64).
+//
+// Row formats follow the reference's stored layouts (nve_types.hpp:143-189,
+// kernels_common.cuh:67-172): a row is `count` values followed by the per-row
+// quantization metadata (scale, then offset when the type has one).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../dtypes.hpp"
+#include "launch.hpp"
+
+namespace nve_amd {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// wave primitives
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Read `v` from lane `src` of the wave (ds_bpermute; every lane of the source
+// group must be active, which the callers guarantee by keeping the branches
+// around a shuffle uniform over a lane group).
+__device__ __forceinline__ uint32_t shfl32(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)v);
+}
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
+  const uint32_t lo = shfl32((uint32_t)v, src);
+  const uint32_t hi = shfl32((uint32_t)(v >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ float shflf(float v, int src) {
+  return __uint_as_float(shfl32(__float_as_uint(v), src));
+}
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint16_t h) {
+  _Float16 x;
+  __builtin_memcpy(&x, &h, 2);
+  return (float)x;
+}
+// binary32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t f2h(float f) {
+  _Float16 x = (_Float16)f;
+  uint16_t h;
+  __builtin_memcpy(&h, &x, 2);
+  return h;
+}
+// OCP FP8 E4M3FN (bias 7, no infinities, NaN = S.1111.111), decoded exactly.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
+  const uint32_t s = (v & 0x80u) << 24;
+  const uint32_t e = (v >> 3) & 0xfu;
+  const uint32_t m = v & 7u;
+  uint32_t bits;
+  if (e == 0) {
+    // m * 2^-9 is exact in binary32
+    return __uint_as_float(s | __float_as_uint((float)m * 0.001953125f));
+  } else if (e == 15 && m == 7) {
+    bits = s | 0x7fc00000u;
+  } else {
+    bits = s | ((e + 120u) << 23) | (m << 20);
+  }
+  return __uint_as_float(bits);
+}
+
+// ---------------------------------------------------------------------------
+// vector loads / stores of VB bytes (VB in {1,2,4,8,16}, address VB-aligned)
+// ---------------------------------------------------------------------------
+template <int VB>
+struct Vec {
+  uint8_t b[VB];
+};
+
+template <int VB>
+__device__ __forceinline__ Vec<VB> load_vec(const uint8_t* p) {
+  Vec<VB> v;
+  if constexpr (VB == 16) {
+    const uint4 x = *reinterpret_cast<const uint4*>(p);
+    __builtin_memcpy(v.b, &x, 16);
+  } else if constexpr (VB == 8) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    __builtin_memcpy(v.b, &x, 8);
+  } else if constexpr (VB == 4) {
+    const uint32_t x = *reinterpret_cast<const uint32_t*>(p);
+    __builtin_memcpy(v.b, &x, 4);
+  } else if constexpr (VB == 2) {
+    const uint16_t x = *reinterpret_cast<const uint16_t*>(p);
+    __builtin_memcpy(v.b, &x, 2);
+  } else {
+    v.b[0] = *p;
+  }
+  return v;
+}
+
+// Streaming store (the output is written once and not re-read by the lookup).
+template <int VB>
+__device__ __forceinline__ void store_vec(uint8_t* p, const Vec<VB>& v) {
+  if constexpr (VB == 16) {
+    uint4 x;
+    __builtin_memcpy(&x, v.b, 16);
+    __builtin_nontemporal_store(x.x, reinterpret_cast<uint32_t*>(p) + 0);
+    __builtin_nontemporal_store(x.y, reinterpret_cast<uint32_t*>(p) + 1);
+    __builtin_nontemporal_store(x.z, reinterpret_cast<uint32_t*>(p) + 2);
+    __builtin_nontemporal_store(x.w, reinterpret_cast<uint32_t*>(p) + 3);
+  } else if constexpr (VB == 8) {
+    uint2 x;
+    __builtin_memcpy(&x, v.b, 8);
+    __builtin_nontemporal_store(x.x, reinterpret_cast<uint32_t*>(p) + 0);
+    __builtin_nontemporal_store(x.y, reinterpret_cast<uint32_t*>(p) + 1);
+  } else if constexpr (VB == 4) {
+    uint32_t x;
+    __builtin_memcpy(&x, v.b, 4);
+    __builtin_nontemporal_store(x, reinterpret_cast<uint32_t*>(p));
+  } else if constexpr (VB == 2) {
+    uint16_t x;
+    __builtin_memcpy(&x, v.b, 2);
+    *reinterpret_cast<uint16_t*>(p) = x;
+  } else {
+    *p = v.b[0];
+  }
+}
+
+// Store E floats (as f32 or RNE f16) at p, which is aligned to E*element bytes.
+template <int E>
+__device__ __forceinline__ void store_out(uint8_t* p, const float* v, bool out_f16) {
+  if (out_f16) {
+    Vec<2 * E> o;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint16_t h = f2h(v[e]);
+      __builtin_memcpy(o.b + 2 * e, &h, 2);
+    }
+    store_vec<2 * E>(p, o);
+  } else {
+    if constexpr (E <= 4) {
+      Vec<4 * E> o;
+      __builtin_memcpy(o.b, v, 4 * E);
+      store_vec<4 * E>(p, o);
+    } else {
+#pragma unroll
+      for (int c = 0; c < E / 4; ++c) {
+        Vec<16> o;
+        __builtin_memcpy(o.b, v + 4 * c, 16);
+        store_vec<16>(p + 16 * c, o);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per-row dequantization: decode the E values of a VB-byte slice of the row's
+// value area into fp32.  Metadata (scale, offset) is read per row.
+// ---------------------------------------------------------------------------
+template <int SDT>
+struct Fmt;
+
+template <>
+struct Fmt<kF32> {
+  static constexpr int esize = 4;
+  static constexpr int meta = 0;
+};
+template <>
+struct Fmt<kF16> {
+  static constexpr int esize = 2;
+  static constexpr int meta = 0;
+};
+template <>
+struct Fmt<kQI8F32> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 4;
+};
+template <>
+struct Fmt<kQI8F16> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 2;
+};
+template <>
+struct Fmt<kQU8F32> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 8;
+};
+template <>
+struct Fmt<kQU8F16> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 4;
+};
+template <>
+struct Fmt<kXI8AF32> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 8;
+};
+template <>
+struct Fmt<kXE4M3F32> {
+  static constexpr int esize = 1;
+  static constexpr int meta = 4;
+};
+
+struct Meta {
+  float s;
+  float o;
+};
+
+// Metadata sits right after the value area; its address is only 2-byte
+// aligned in general, so it is assembled from 16-bit loads.
+__device__ __forceinline__ float ld_f32_unaligned(const uint8_t* p) {
+  const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+  const uint32_t v = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+  return __uint_as_float(v);
+}
+
+template <int SDT>
+__device__ __forceinline__ Meta load_meta(const uint8_t* row, int64_t value_bytes) {
+  Meta m{1.0f, 0.0f};
+  const uint8_t* p = row + value_bytes;
+  if constexpr (SDT == kQI8F32 || SDT == kXE4M3F32) {
+    m.s = ld_f32_unaligned(p);
+  } else if constexpr (SDT == kQU8F32 || SDT == kXI8AF32) {
+    m.s = ld_f32_unaligned(p);
+    m.o = ld_f32_unaligned(p + 4);
+  } else if constexpr (SDT == kQI8F16) {
+    m.s = h2f(*reinterpret_cast<const uint16_t*>(p));
+  } else if constexpr (SDT == kQU8F16) {
+    m.s = h2f(*reinterpret_cast<const uint16_t*>(p));
+    m.o = h2f(*reinterpret_cast<const uint16_t*>(p + 2));
+  }
+  return m;
+}
+
+// Decoded element formulas (kernels_common.cuh:174-297):
+//   F32/F16    the stored value
+//   QI8 F32    fma(q, s, 0)               (float(q)*scale + 0, contracted)
+//   QU8 F32    fma(q, s, o)
+//   QI8 F16    half(float(q) * s)          rounded to half once, then widened
+//   QU8 F16    half(fma(q, s, o))
+//   XI8A F32   fma(q, s, o)                (extension: int8 affine)
+//   XE4M3 F32  e4m3(q) * s                 (extension: OCP fp8 with scale)
+template <int SDT, int VB>
+__device__ __forceinline__ void decode(const Vec<VB>& v, const Meta& m,
+                                       float (&x)[VB / Fmt<SDT>::esize]) {
+  constexpr int E = VB / Fmt<SDT>::esize;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if constexpr (SDT == kF32) {
+      float f;
+      __builtin_memcpy(&f, v.b + 4 * e, 4);
+      x[e] = f;
+    } else if constexpr (SDT == kF16) {
+      uint16_t h;
+      __builtin_memcpy(&h, v.b + 2 * e, 2);
+      x[e] = h2f(h);
+    } else if constexpr (SDT == kQI8F32) {
+      x[e] = __builtin_fmaf((float)(int8_t)v.b[e], m.s, 0.0f);
+    } else if constexpr (SDT == kQU8F32 || SDT == kXI8AF32) {
+      const float q = (SDT == kQU8F32) ? (float)v.b[e] : (float)(int8_t)v.b[e];
+      x[e] = __builtin_fmaf(q, m.s, m.o);
+    } else if constexpr (SDT == kQI8F16) {
+      x[e] = h2f(f2h((float)(int8_t)v.b[e] * m.s));
+    } else if constexpr (SDT == kQU8F16) {
+      x[e] = h2f(f2h(__builtin_fmaf((float)v.b[e], m.s, m.o)));
+    } else if constexpr (SDT == kXE4M3F32) {
+      x[e] = e4m3_to_f32(v.b[e]) * m.s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// key / row resolution
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t load_key(const void* keys, int key_bytes, int64_t i) {
+  return key_bytes == 4 ? (int64_t) reinterpret_cast<const int32_t*>(keys)[i]
+                        : reinterpret_cast<const int64_t*>(keys)[i];
+}
+
+// Where rows come from (RowSource, launch.hpp).  Without a cache: row =
+// table + index*row_bytes, index being the key (load_indices) or the key's
+// position (a buffer gathered earlier).  With a cache (EmbedCacheSA layout,
+// ec_set_associative.h:104-112, ec_set_associative.cuh:46-80): 8 tags per set
+// at tags + set*8, rows at data + (set*8 + way)*row_bytes;
+// set = (unsigned)key % num_sets; a hit is the lowest way whose rebuilt key
+// tag*num_sets + set equals the key; a miss resolves to table + key*row_bytes,
+// or to nothing when table is null.
+// Returns the row address (0 when unresolved); *hit reports a cache hit or a
+// linear-table row; *miss a cache miss (whether or not a backing row exists).
+__device__ __forceinline__ uint64_t resolve_row(const RowSource& src, int key_bytes, int64_t key,
+                                                int64_t pos, bool* miss) {
+  *miss = false;
+  if (src.cache_data == nullptr) {
+    const uint64_t idx = src.load_indices ? (uint64_t)key : (uint64_t)pos;
+    return (uint64_t)src.table + idx * src.row_bytes;
+  }
+  uint32_t set;
+  uint32_t mask = 0;
+  if (key_bytes == 4) {
+    const uint32_t uk = (uint32_t)(int32_t)key;
+    const uint32_t ns = (uint32_t)src.num_sets;
+    set = uk % ns;
+    const uint4* tp = reinterpret_cast<const uint4*>(
+        reinterpret_cast<const int32_t*>(src.cache_tags) + (uint64_t)set * 8);
+    const uint4 t0 = tp[0];
+    const uint4 t1 = tp[1];
+    const uint32_t t[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * ns + set == uk) << w;
+  } else {
+    const uint64_t uk = (uint64_t)key;
+    set = (uint32_t)(uk % src.num_sets);
+    const uint4* tp = reinterpret_cast<const uint4*>(
+        reinterpret_cast<const int64_t*>(src.cache_tags) + (uint64_t)set * 8);
+    uint64_t t[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 q = tp[c];
+      t[2 * c] = (uint64_t)q.x | ((uint64_t)q.y << 32);
+      t[2 * c + 1] = (uint64_t)q.z | ((uint64_t)q.w << 32);
+    }
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * src.num_sets + set == uk) << w;
+  }
+  if (mask) {
+    const uint32_t way = (uint32_t)__builtin_ctz(mask);
+    return (uint64_t)src.cache_data + ((uint64_t)set * 8 + way) * src.row_bytes;
+  }
+  *miss = true;
+  return src.table ? (uint64_t)src.table + (uint64_t)key * src.row_bytes : 0;
+}
+
+}  // namespace nve_amd

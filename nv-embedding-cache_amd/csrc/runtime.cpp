@@ -1,0 +1,231 @@
+// runtime.cpp -- see runtime.hpp.
+#include "runtime.hpp"
+
+#include "kernels/cache_launch.hpp"
+
+#include <cstdlib>
+#include <cstring>
+
+namespace nve_amd {
+
+ScopedDevice::ScopedDevice(int device) {
+  if (device < 0) return;
+  NVE_HIP(hipGetDevice(&prev_));
+  if (prev_ != device) {
+    NVE_HIP(hipSetDevice(device));
+  } else {
+    prev_ = -1;
+  }
+}
+
+ScopedDevice::~ScopedDevice() {
+  if (prev_ >= 0) (void)hipSetDevice(prev_);
+}
+
+// ---------------------------------------------------------------------------
+ThreadPool::ThreadPool(int64_t num_workers) {
+  if (num_workers <= 0) {
+    const int64_t cores = (int64_t)std::thread::hardware_concurrency();
+    num_workers = cores - 2 > 1 ? cores - 2 : 1;  // thread_pool.cpp:112-116
+  }
+  for (int64_t i = 0; i < num_workers; ++i) workers_.emplace_back(&ThreadPool::main_, this);
+}
+
+ThreadPool::~ThreadPool() {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    stop_ = true;
+  }
+  cv_.notify_all();
+  for (auto& t : workers_) t.join();
+}
+
+std::future<void> ThreadPool::submit(std::function<void()> task) {
+  std::packaged_task<void()> pt(std::move(task));
+  auto f = pt.get_future();
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    queue_.emplace_back(std::move(pt));
+  }
+  cv_.notify_one();
+  return f;
+}
+
+void ThreadPool::main_() {
+  for (;;) {
+    std::packaged_task<void()> t;
+    {
+      std::unique_lock<std::mutex> lk(mu_);
+      cv_.wait(lk, [&] { return stop_ || !queue_.empty(); });
+      if (queue_.empty()) return;
+      t = std::move(queue_.front());
+      queue_.pop_front();
+    }
+    t();
+  }
+}
+
+namespace {
+std::mutex g_pool_mu;
+std::shared_ptr<ThreadPool> g_pool;
+int64_t g_pool_workers = 0;
+}  // namespace
+
+std::shared_ptr<ThreadPool> ThreadPool::default_pool() {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  if (!g_pool) g_pool = std::make_shared<ThreadPool>(g_pool_workers);
+  return g_pool;
+}
+
+void ThreadPool::configure_default(int64_t num_workers) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  NVE_CHECK(!g_pool, "The default thread pool is already in use");
+  g_pool_workers = num_workers;
+}
+
+int64_t json_int_field(const char* json, const char* field, int64_t dflt) {
+  if (json == nullptr) return dflt;
+  const std::string s(json);
+  const std::string q = std::string("\"") + field + "\"";
+  const size_t at = s.find(q);
+  if (at == std::string::npos) return dflt;
+  size_t i = s.find(':', at + q.size());
+  NVE_CHECK_ARG(i != std::string::npos, "Malformed JSON near '", field, "'");
+  ++i;
+  while (i < s.size() && (s[i] == ' ' || s[i] == '\t' || s[i] == '\n')) ++i;
+  char* end = nullptr;
+  const long long v = std::strtoll(s.c_str() + i, &end, 10);
+  NVE_CHECK_ARG(end != s.c_str() + i, "JSON field '", field, "' must be an integer");
+  return (int64_t)v;
+}
+
+// ---------------------------------------------------------------------------
+ExecutionContext::ExecutionContext(int device, hipStream_t lookup, hipStream_t modify,
+                                   std::shared_ptr<ThreadPool> pool)
+    : device_(device), lookup_(lookup), modify_(modify), pool_(std::move(pool)) {
+  if (!pool_) pool_ = ThreadPool::default_pool();
+}
+
+ExecutionContext::~ExecutionContext() {
+  try {
+    wait();
+  } catch (...) {
+  }
+  ScopedDevice sd(device_);
+  for (auto& kv : bufs_) {
+    if (kv.second.host)
+      (void)hipHostFree(kv.second.ptr);
+    else
+      (void)hipFree(kv.second.ptr);
+  }
+  if (misses_) (void)hipFree(misses_);
+}
+
+void* ExecutionContext::buffer(const std::string& name, size_t bytes, bool host) {
+  Buf& b = bufs_[name];
+  if (b.ptr && (b.bytes < bytes || b.host != host)) {
+    // the stream may still use the old buffer
+    NVE_HIP(hipStreamSynchronize(lookup_));
+    NVE_HIP(hipStreamSynchronize(modify_));
+    if (b.host)
+      NVE_HIP(hipHostFree(b.ptr));
+    else
+      NVE_HIP(hipFree(b.ptr));
+    b.ptr = nullptr;
+  }
+  if (!b.ptr) {
+    const size_t sz = bytes > 256 ? bytes : 256;
+    if (host)
+      NVE_HIP(hipHostMalloc(&b.ptr, sz, hipHostMallocDefault));
+    else
+      NVE_HIP(hipMalloc(&b.ptr, sz));
+    b.bytes = sz;
+    b.host = host;
+  }
+  return b.ptr;
+}
+
+unsigned long long* ExecutionContext::miss_counter() {
+  if (!misses_) {
+    NVE_HIP(hipMalloc(&misses_, sizeof(unsigned long long)));
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(misses_), 1, 0, lookup_));
+  }
+  return misses_;
+}
+
+void ExecutionContext::reset_misses() {
+  // a fill kernel rather than a memset node, so the lookup stays capturable
+  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(miss_counter()), 1, 0, lookup_));
+}
+
+int64_t ExecutionContext::read_misses() {
+  unsigned long long h = 0;
+  NVE_HIP(hipMemcpyAsync(&h, miss_counter(), sizeof(h), hipMemcpyDeviceToHost, lookup_));
+  NVE_HIP(hipStreamSynchronize(lookup_));
+  return (int64_t)h;
+}
+
+void ExecutionContext::add_pending(std::future<void> f) {
+  std::lock_guard<std::mutex> lk(pending_mu_);
+  pending_.push_back(std::move(f));
+}
+
+void ExecutionContext::wait() {
+  std::vector<std::future<void>> fs;
+  {
+    std::lock_guard<std::mutex> lk(pending_mu_);
+    fs.swap(pending_);
+  }
+  std::exception_ptr first;
+  for (auto& f : fs) {
+    try {
+      f.get();
+    } catch (...) {
+      if (!first) first = std::current_exception();
+    }
+  }
+  ScopedDevice sd(device_);
+  NVE_HIP(hipStreamSynchronize(lookup_));
+  NVE_HIP(hipStreamSynchronize(modify_));
+  if (first) std::rethrow_exception(first);
+}
+
+// ---------------------------------------------------------------------------
+MemKind mem_kind(const void* p) {
+  hipPointerAttribute_t attr;
+  std::memset(&attr, 0, sizeof(attr));
+  const hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // clear: an unknown pointer is plain host memory
+    return MemKind::PageableHost;
+  }
+  switch (attr.type) {
+    case hipMemoryTypeDevice:
+    case hipMemoryTypeManaged:
+    case hipMemoryTypeUnified: return MemKind::Device;
+    case hipMemoryTypeHost: return MemKind::PinnedHost;
+    default: return MemKind::PageableHost;
+  }
+}
+
+const void* device_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
+                         hipStream_t stream) {
+  if (p == nullptr || bytes == 0) return p;
+  if (mem_kind(p) == MemKind::Device) return p;
+  void* d = ctx.buffer(name, bytes, false);
+  NVE_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream));
+  return d;
+}
+
+void* device_output(ExecutionContext& ctx, const char* name, void* p, size_t bytes) {
+  if (p == nullptr || bytes == 0) return p;
+  if (mem_kind(p) == MemKind::Device) return p;
+  return ctx.buffer(name, bytes, false);
+}
+
+void finish_output(void* user, const void* dev, size_t bytes, hipStream_t stream) {
+  if (user == dev || bytes == 0) return;
+  NVE_HIP(hipMemcpyAsync(user, dev, bytes, hipMemcpyDeviceToHost, stream));
+}
+
+}  // namespace nve_amd

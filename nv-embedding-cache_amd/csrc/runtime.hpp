@@ -1,0 +1,162 @@
+// runtime.hpp -- host runtime of the MI355X lookup library: errors, thread
+// pool, execution contexts and buffer staging.
+//
+// Reference counterparts (file:line in /root/reference):
+//   errors -> C status      src/nve_c_api_internal.hpp:48-92, include/common.hpp
+//   thread pool             include/thread_pool.hpp:50-151, src/thread_pool.cpp:97-160
+//   execution context       include/execution_context.hpp:34-84, include/layer_utils.hpp:66-199
+//   buffer staging          include/buffer_wrapper.hpp:34-123
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <condition_variable>
+#include <deque>
+#include <functional>
+#include <future>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/nve_c_api.h"
+
+namespace nve_amd {
+
+// ---------------------------------------------------------------------------
+// errors: each carries the C status it maps to
+// ---------------------------------------------------------------------------
+class Error : public std::runtime_error {
+ public:
+  Error(nve_status_t status, const std::string& msg) : std::runtime_error(msg), status_(status) {}
+  nve_status_t status() const { return status_; }
+
+ private:
+  nve_status_t status_;
+};
+
+template <typename... T>
+std::string cat(const T&... parts) {
+  std::ostringstream os;
+  (os << ... << parts);
+  return os.str();
+}
+
+#define NVE_CHECK_ARG(cond, ...)                                                        \
+  do {                                                                                  \
+    if (!(cond)) throw ::nve_amd::Error(NVE_ERROR_INVALID_ARGUMENT, ::nve_amd::cat(__VA_ARGS__)); \
+  } while (0)
+#define NVE_CHECK(cond, ...)                                                        \
+  do {                                                                              \
+    if (!(cond)) throw ::nve_amd::Error(NVE_ERROR_RUNTIME, ::nve_amd::cat(__VA_ARGS__)); \
+  } while (0)
+#define NVE_NOT_IMPLEMENTED(...) \
+  throw ::nve_amd::Error(NVE_ERROR_NOT_IMPLEMENTED, ::nve_amd::cat(__VA_ARGS__))
+#define NVE_HIP(expr)                                                                        \
+  do {                                                                                       \
+    const hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                                    \
+      throw ::nve_amd::Error(e_ == hipErrorOutOfMemory ? NVE_ERROR_OUT_OF_MEMORY : NVE_ERROR_CUDA, \
+                             ::nve_amd::cat(#expr, ": ", hipGetErrorName(e_), " (",              \
+                                            hipGetErrorString(e_), ")"));                    \
+  } while (0)
+
+// Makes `device` current for the scope (ScopedDevice, include/cuda_support.hpp).
+class ScopedDevice {
+ public:
+  explicit ScopedDevice(int device);
+  ~ScopedDevice();
+
+ private:
+  int prev_ = -1;
+};
+
+// ---------------------------------------------------------------------------
+// thread pool (SimpleThreadPool: default workers = max(cores - 2, 1))
+// ---------------------------------------------------------------------------
+class ThreadPool {
+ public:
+  explicit ThreadPool(int64_t num_workers);
+  ~ThreadPool();
+  std::future<void> submit(std::function<void()> task);
+  int64_t num_workers() const { return (int64_t)workers_.size(); }
+
+  static std::shared_ptr<ThreadPool> default_pool();
+  static void configure_default(int64_t num_workers);
+
+ private:
+  void main_();
+  std::vector<std::thread> workers_;
+  std::deque<std::packaged_task<void()>> queue_;
+  std::mutex mu_;
+  std::condition_variable cv_;
+  bool stop_ = false;
+};
+
+// Minimal reader of the thread-pool JSON ({"num_workers": N, ...}).
+int64_t json_int_field(const char* json, const char* field, int64_t dflt);
+
+// ---------------------------------------------------------------------------
+// execution context: streams, named grow-only scratch buffers, a miss counter
+// and the futures of work handed to the thread pool.
+// ---------------------------------------------------------------------------
+class ExecutionContext {
+ public:
+  ExecutionContext(int device, hipStream_t lookup, hipStream_t modify,
+                   std::shared_ptr<ThreadPool> pool);
+  virtual ~ExecutionContext();
+
+  int device() const { return device_; }
+  hipStream_t lookup_stream() const { return lookup_; }
+  hipStream_t modify_stream() const { return modify_; }
+  ThreadPool& pool() { return *pool_; }
+
+  // Device (host = false) or pinned host (host = true) buffer of at least
+  // `bytes`, kept under `name` and reused by later calls on this context.
+  void* buffer(const std::string& name, size_t bytes, bool host = false);
+
+  // Device counter of cache misses (zeroed by reset_misses on lookup_stream).
+  unsigned long long* miss_counter();
+  void reset_misses();
+  int64_t read_misses();  // syncs lookup_stream
+
+  void add_pending(std::future<void> f);
+  void wait();
+
+ private:
+  struct Buf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool host = false;
+  };
+  int device_;
+  hipStream_t lookup_, modify_;
+  std::shared_ptr<ThreadPool> pool_;
+  std::map<std::string, Buf> bufs_;
+  unsigned long long* misses_ = nullptr;
+  std::mutex pending_mu_;
+  std::vector<std::future<void>> pending_;
+};
+
+// ---------------------------------------------------------------------------
+// staging of caller buffers that may live in host or device memory
+// ---------------------------------------------------------------------------
+enum class MemKind { Device, PinnedHost, PageableHost };
+MemKind mem_kind(const void* p);
+
+// Device-readable view of `bytes` at `p`: p itself when the GPU can read it,
+// else a copy into the context buffer `name` (queued on `stream`).
+const void* device_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
+                         hipStream_t stream);
+
+// Device-writable target for `bytes` at `p`; when it differs from p, call
+// finish_output afterwards to copy it back.
+void* device_output(ExecutionContext& ctx, const char* name, void* p, size_t bytes);
+void finish_output(void* user, const void* dev, size_t bytes, hipStream_t stream);
+
+}  // namespace nve_amd

@@ -1,0 +1,214 @@
+"""GPU parity of the set-associative cache lookups (tag compare, set/tag math,
+row layout, misses served from the host-linear backing table, miss counts)
+against the oracle's cache model.
+
+The cache content is produced by the oracle (its insert model) and loaded into
+the GPU table with nve_amd_gpu_table_import_state plus a row copy, so these
+tests pin the lookup side independently of the GPU insert.  Cases follow
+tests/ecache/api_test.cu (lookup, UVM lookup, negative keys) and
+tests/gpu_table/gpu_table_test.cpp (find with hit mask, find_uvm, combine)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from nve_helpers import (csr_offsets, float_table, hip_memcpy, quant_table, stream_ptr, to_dev, vp)
+from oracle import oracle as O
+from pynve import _lib
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+class CachedTable:
+    """GPU table (+ optional pinned backing table) whose cache state is copied
+    from an oracle cache model."""
+
+    def __init__(self, uvm_bytes, cache_bytes, key_bytes=8, with_uvm=True, value_dtype=_lib.DT_F32):
+        self.rows, self.width = uvm_bytes.shape
+        self.key_bytes = key_bytes
+        self.uvm_np = np.ascontiguousarray(uvm_bytes)
+        self.h_uvm = torch.from_numpy(self.uvm_np.reshape(-1).copy()).pin_memory() if with_uvm else None
+        L = _lib.load()
+        cfg = L.nve_gpu_table_config_default()
+        cfg.cache_size = cache_bytes
+        cfg.row_size_in_bytes = self.width
+        cfg.value_dtype = value_dtype
+        if with_uvm:
+            cfg.uvm_table = self.h_uvm.data_ptr()
+            cfg.uvm_num_rows = self.rows
+        self.table = ctypes.c_void_p()
+        kt = _lib.KEY_INT32 if key_bytes == 4 else _lib.KEY_INT64
+        _lib.call("nve_gpu_table_create", ctypes.byref(self.table), kt, ctypes.byref(cfg), None)
+        self.ctx = ctypes.c_void_p()
+        s = stream_ptr()
+        _lib.call("nve_table_create_execution_context", self.table, ctypes.byref(self.ctx), s, s, None, None)
+        ns = ctypes.c_int64()
+        _lib.call("nve_amd_gpu_table_num_sets", self.table, ctypes.byref(ns))
+        self.num_sets = ns.value
+        self.model = O.Cache(cache_bytes, self.width, key_bytes)
+        assert self.model.num_sets == self.num_sets
+
+    def load_model(self):
+        """Copy the oracle cache's tags and rows into the GPU table."""
+        tags = self.model.tags()
+        if self.key_bytes == 4:
+            tags = tags.astype(np.int32)
+        _lib.call("nve_amd_gpu_table_import_state", self.table, tags.ctypes.data_as(ctypes.c_void_p),
+                  None, None, 0)
+        data = ctypes.c_void_p()
+        _lib.call("nve_amd_gpu_table_data", self.table, ctypes.byref(data))
+        d = self.model.data()
+        hip_memcpy(data.value, d.ctypes.data, d.nbytes)
+
+    def close(self):
+        _lib.call("nve_context_wait", self.ctx)
+        _lib.call("nve_context_destroy", self.ctx)
+        _lib.call("nve_table_destroy", self.table)
+
+
+def warm(ct, rng, n_insert, hot_rows, elem_bytes=4):
+    """Insert with the oracle's policy, then negate every cached value (sign
+    bit flip) so that a cache row and its backing row differ: a wrong hit/miss
+    decision then changes the output."""
+    keys = rng.choice(hot_rows, size=n_insert).astype(np.int64 if ct.key_bytes == 8 else np.int32)
+    ct.model.insert_keys(keys, uvm=ct.uvm_np.reshape(-1))
+    d = ct.model.data()
+    d.reshape(-1, elem_bytes)[:, elem_bytes - 1] ^= np.uint8(0x80)
+    ct.load_model()
+
+
+def test_num_sets_matches_reference_formula():
+    # ec_set_associative.h:667-685 + device-modify counters: per set
+    # align16(8*8) + align16(8*256) + align16(8*4) = 2144 bytes for int64 keys
+    ct = CachedTable(np.zeros((10, 256), np.uint8), 2144 * 1000 + 2143)
+    assert ct.num_sets == 1000
+    ct.close()
+
+
+@pytest.mark.parametrize("key_bytes", [8, 4])
+def test_find_uvm_resolves_hits_from_cache_and_misses_from_host(key_bytes):
+    rng = np.random.default_rng(5 + key_bytes)
+    rows, dim = 20000, 64
+    uvm = float_table(rng, rows, dim, O.F32, dyadic_values=False)
+    ct = CachedTable(uvm, 300 * 1024, key_bytes)
+    warm(ct, rng, 4000, np.arange(0, 3000))
+    kdt = np.int64 if key_bytes == 8 else np.int32
+    keys = rng.integers(0, rows, size=5000).astype(kdt)
+    keys[:2500] = rng.integers(0, 3000, size=2500)
+    rows_ptr, hits, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    out = torch.zeros((keys.size, dim * 4), dtype=torch.uint8, device="cuda")
+    _lib.call("nve_table_reset_lookup_counter", ct.table, ct.ctx)
+    _lib.call("nve_table_find", ct.table, ct.ctx, keys.size, vp(to_dev(keys)), None, dim * 4, vp(out), None)
+    cnt = ctypes.c_int64()
+    _lib.call("nve_table_get_lookup_counter", ct.table, ct.ctx, ctypes.byref(cnt))
+    got = out.cpu().numpy()
+    # expected rows: cache slot or backing row, as the model resolves them
+    data = ct.model.data()
+    base_d, base_u = data.ctypes.data, ct.uvm_np.ctypes.data
+    for i in range(keys.size):
+        p = int(rows_ptr[i])
+        if base_d <= p < base_d + data.nbytes:
+            exp = data[p - base_d:p - base_d + dim * 4]
+        else:
+            exp = ct.uvm_np.reshape(-1)[p - base_u:p - base_u + dim * 4]
+        assert np.array_equal(got[i], exp), i
+    assert cnt.value == misses
+    assert 0 < misses < keys.size
+    ct.close()
+
+
+def test_find_without_backing_sets_hit_mask_and_keeps_missed_rows():
+    rng = np.random.default_rng(17)
+    rows, dim = 5000, 32
+    uvm = float_table(rng, rows, dim, O.F32)
+    ct = CachedTable(uvm, 64 * 1024, 8, with_uvm=False)
+    warm(ct, rng, 800, np.arange(0, 600))
+    keys = rng.integers(0, 1200, size=1000).astype(np.int64)
+    mask_in = np.zeros((1000 + 63) // 64, np.uint64)
+    mask_in[0] = np.uint64(0xFF)  # first 8 keys already resolved: skipped
+    d_mask = to_dev(mask_in)
+    out = torch.full((1000, dim * 4), 0xAB, dtype=torch.uint8, device="cuda")
+    _lib.call("nve_table_find", ct.table, ct.ctx, 1000, vp(to_dev(keys)), vp(d_mask), dim * 4, vp(out), None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    data = ct.model.data()
+    mask = d_mask.cpu().numpy().view(np.uint64)
+    for i, k in enumerate(keys.tolist()):
+        bit = (int(mask[i // 64]) >> (i % 64)) & 1
+        if i < 8:
+            assert bit == 1 and np.all(got[i] == 0xAB)
+            continue
+        way = ct.model.find_way(k)
+        if way < 0:
+            assert bit == 0 and np.all(got[i] == 0xAB)
+        else:
+            slot = ct.model.set_of(k) * 8 + way
+            assert bit == 1 and np.array_equal(got[i], data[slot * dim * 4:(slot + 1) * dim * 4])
+    ct.close()
+
+
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_WMEAN, _lib.POOL_CONCAT])
+def test_uvm_layer_pooled_and_hitrate(pooling):
+    rng = np.random.default_rng(23 + pooling)
+    rows, dim, bags = 30000, 128, 400
+    uvm = float_table(rng, rows, dim, O.F16, dyadic_values=False)
+    ct = CachedTable(uvm, 2 * 1024 * 1024, 8, value_dtype=_lib.DT_F16)
+    warm(ct, rng, 20000, np.arange(0, 8000), elem_bytes=2)
+    off = csr_offsets(rng, bags, 30)
+    n = int(off[-1])
+    keys = np.where(rng.uniform(size=n) < 0.8, rng.integers(0, 8000, size=n),
+                    rng.integers(0, rows, size=n)).astype(np.int64)
+    w = rng.uniform(0, 1, size=n).astype(np.float32)
+    L = _lib.load()
+    never = ctypes.c_void_p()
+    _lib.call("nve_heuristic_create_never", ctypes.byref(never))
+    lc = L.nve_linear_uvm_layer_config_default()
+    lc.insert_heuristic = never.value
+    layer = ctypes.c_void_p()
+    _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), ct.table, None)
+    _lib.call("nve_heuristic_destroy", never)
+    lctx = ctypes.c_void_p()
+    s = stream_ptr()
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
+    hr = (ctypes.c_float * 1)()
+    rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    if pooling == _lib.POOL_CONCAT:
+        out = torch.zeros((n, dim), dtype=torch.float16, device="cuda")
+        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(to_dev(keys)), vp(out), dim * 2, None, pooling,
+                  0, None, 0, 0, None, 0, _lib.DT_F16, hr)
+        got = out.cpu().numpy().view(np.uint16)
+        ref = np.stack([np.frombuffer(ctypes.string_at(int(p), dim * 2), np.uint16) for p in rows_ptr])
+        assert np.array_equal(got, ref)
+    else:
+        out = torch.zeros((bags, dim), dtype=torch.float16, device="cuda")
+        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(to_dev(keys)), vp(out), dim * 2, None, pooling,
+                  _lib.SPARSE_CSR, vp(to_dev(off)), bags + 1, 0, vp(to_dev(w)), _lib.DT_F32, _lib.DT_F16, hr)
+        got = out.cpu().numpy().view(np.uint16)
+        ref = O.pool(rows_ptr, O.F16, dim, O.CSR, pooling, n, off, bags, 0, w, O.F32, O.F16)
+        assert np.array_equal(got, ref)
+    assert abs(hr[0] - (1.0 - misses / n)) < 1e-6
+    _lib.call("nve_context_wait", lctx)
+    _lib.call("nve_context_destroy", lctx)
+    _lib.call("nve_layer_destroy", layer)
+    ct.close()
+
+
+def test_erase_and_clear():
+    rng = np.random.default_rng(41)
+    rows, dim = 4000, 16
+    uvm = float_table(rng, rows, dim, O.F32)
+    ct = CachedTable(uvm, 32 * 1024, 8)
+    warm(ct, rng, 600, np.arange(0, 500))
+    cached = [k for k in range(500) if ct.model.find_way(k) >= 0]
+    assert len(cached) > 20
+    erase = np.array(cached[:10], np.int64)
+    _lib.call("nve_table_erase", ct.table, ct.ctx, erase.size, vp(to_dev(erase)))
+    ct.model.erase(erase)
+    tags = np.zeros(ct.num_sets * 8, np.int64)
+    _lib.call("nve_amd_gpu_table_export_state", ct.table, tags.ctypes.data_as(ctypes.c_void_p), None, None, None)
+    assert np.array_equal(tags, ct.model.tags())
+    _lib.call("nve_table_clear", ct.table, ct.ctx)
+    _lib.call("nve_amd_gpu_table_export_state", ct.table, tags.ctypes.data_as(ctypes.c_void_p), None, None, None)
+    assert np.all(tags == -1)
+    ct.close()
