@@ -99,7 +99,8 @@ def test_find_uvm_resolves_hits_from_cache_and_misses_from_host(key_bytes):
     rows_ptr, hits, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
     out = torch.zeros((keys.size, dim * 4), dtype=torch.uint8, device="cuda")
     _lib.call("nve_table_reset_lookup_counter", ct.table, ct.ctx)
-    _lib.call("nve_table_find", ct.table, ct.ctx, keys.size, vp(to_dev(keys)), None, dim * 4, vp(out), None)
+    d_keys = to_dev(keys)  # keep device inputs referenced until the call has run
+    _lib.call("nve_table_find", ct.table, ct.ctx, keys.size, vp(d_keys), None, dim * 4, vp(out), None)
     cnt = ctypes.c_int64()
     _lib.call("nve_table_get_lookup_counter", ct.table, ct.ctx, ctypes.byref(cnt))
     got = out.cpu().numpy()
@@ -129,7 +130,8 @@ def test_find_without_backing_sets_hit_mask_and_keeps_missed_rows():
     mask_in[0] = np.uint64(0xFF)  # first 8 keys already resolved: skipped
     d_mask = to_dev(mask_in)
     out = torch.full((1000, dim * 4), 0xAB, dtype=torch.uint8, device="cuda")
-    _lib.call("nve_table_find", ct.table, ct.ctx, 1000, vp(to_dev(keys)), vp(d_mask), dim * 4, vp(out), None)
+    d_keys = to_dev(keys)
+    _lib.call("nve_table_find", ct.table, ct.ctx, 1000, vp(d_keys), vp(d_mask), dim * 4, vp(out), None)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     data = ct.model.data()
@@ -173,17 +175,18 @@ def test_uvm_layer_pooled_and_hitrate(pooling):
     _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
     hr = (ctypes.c_float * 1)()
     rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    d_keys, d_off, d_w = to_dev(keys), to_dev(off), to_dev(w)
     if pooling == _lib.POOL_CONCAT:
         out = torch.zeros((n, dim), dtype=torch.float16, device="cuda")
-        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(to_dev(keys)), vp(out), dim * 2, None, pooling,
+        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), dim * 2, None, pooling,
                   0, None, 0, 0, None, 0, _lib.DT_F16, hr)
         got = out.cpu().numpy().view(np.uint16)
         ref = np.stack([np.frombuffer(ctypes.string_at(int(p), dim * 2), np.uint16) for p in rows_ptr])
         assert np.array_equal(got, ref)
     else:
         out = torch.zeros((bags, dim), dtype=torch.float16, device="cuda")
-        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(to_dev(keys)), vp(out), dim * 2, None, pooling,
-                  _lib.SPARSE_CSR, vp(to_dev(off)), bags + 1, 0, vp(to_dev(w)), _lib.DT_F32, _lib.DT_F16, hr)
+        _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), dim * 2, None, pooling,
+                  _lib.SPARSE_CSR, vp(d_off), bags + 1, 0, vp(d_w), _lib.DT_F32, _lib.DT_F16, hr)
         got = out.cpu().numpy().view(np.uint16)
         ref = O.pool(rows_ptr, O.F16, dim, O.CSR, pooling, n, off, bags, 0, w, O.F32, O.F16)
         assert np.array_equal(got, ref)
@@ -203,7 +206,8 @@ def test_erase_and_clear():
     cached = [k for k in range(500) if ct.model.find_way(k) >= 0]
     assert len(cached) > 20
     erase = np.array(cached[:10], np.int64)
-    _lib.call("nve_table_erase", ct.table, ct.ctx, erase.size, vp(to_dev(erase)))
+    d_erase = to_dev(erase)
+    _lib.call("nve_table_erase", ct.table, ct.ctx, erase.size, vp(d_erase))
     ct.model.erase(erase)
     tags = np.zeros(ct.num_sets * 8, np.int64)
     _lib.call("nve_amd_gpu_table_export_state", ct.table, tags.ctypes.data_as(ctypes.c_void_p), None, None, None)
