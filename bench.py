@@ -92,35 +92,39 @@ def cpu_baseline(torch, d_table, key_batches, bags, hot, rows, dim, seconds):
                       f"in {el:.1f} s on '{model}' ({avail} cores available, {threads} worker threads)"}
 
 
-def read_ceiling(torch, lib, stream, seconds_cap=2.0):
-    """Random-row read ceiling: uniform random 256-byte rows from a 16 GiB buffer."""
+def read_ceiling(torch, lib, stream, counts):
+    """Random-row read ceiling: uniform random 256-byte rows of a 16 GiB buffer
+    (far beyond the 256 MB MALL), read by a kernel that does nothing else.
+    Returns {rows_per_launch: (GB/s, us per launch)}."""
     row_bytes = 256
     rows = (16 << 30) // row_bytes
     buf = torch.empty(rows * row_bytes // 2, dtype=torch.int16, device="cuda")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(7)
-    n = 262144 * 4
-    idx = torch.randint(0, rows, (n,), device="cuda", generator=gen, dtype=torch.int64)
-    sink = torch.zeros((n + 127) // 128, dtype=torch.int32, device="cuda")
     s = ctypes.c_void_p(stream.cuda_stream)
+    res = {}
+    for n in counts:
+        idx = torch.randint(0, rows, (n,), device="cuda", generator=gen, dtype=torch.int64)
+        sink = torch.zeros((n + 127) // 128, dtype=torch.int32, device="cuda")
 
-    def launch():
-        lib.call("nve_amd_read_ceiling", ctypes.c_void_p(buf.data_ptr()), row_bytes,
-                 ctypes.c_void_p(idx.data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
+        def launch():
+            lib.call("nve_amd_read_ceiling", ctypes.c_void_p(buf.data_ptr()), row_bytes,
+                     ctypes.c_void_p(idx.data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
 
-    for _ in range(5):
-        launch()
-    reps = 50
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        launch()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+        for _ in range(5):
+            launch()
+        reps = 100
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[n] = ((n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms * 1e3)
     del buf
     torch.cuda.empty_cache()
-    return (n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms
+    return res
 
 
 def main():
@@ -137,6 +141,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run torch's device copy of a 1 GiB buffer 5 times (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -151,6 +158,14 @@ def main():
     _lib.load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}), flush=True)
+        return
     rows, dim, bags, hot = args.rows, args.dim, args.bags, args.hotness
     nkeys = bags * hot
     width = dim * 2
@@ -231,10 +246,15 @@ def main():
                          "output_dtype": "f16", "accumulate": "f32", "key_batches_cycled": args.batches},
               "roofline": roof}
     if not args.no_ceiling:
-        ceil, cms = read_ceiling(torch, _lib, stream)
-        log(f"random-row read ceiling: {ceil:.0f} GB/s ({cms * 1000:.1f} us per 1M rows)")
-        result["ceiling"] = {"random_row_read_GBps": round(ceil, 1),
-                             "frac_of_ceiling": round(achieved / ceil, 4)}
+        # same number of rows per launch as one batch, and 4x that (closer to asymptotic)
+        c = read_ceiling(torch, _lib, stream, [nkeys, 4 * nkeys])
+        (c1, us1), (c4, us4) = c[nkeys], c[4 * nkeys]
+        log(f"random-row read ceiling: {c1:.0f} GB/s at {nkeys} rows/launch ({us1:.1f} us), "
+            f"{c4:.0f} GB/s at {4 * nkeys} rows/launch ({us4:.1f} us)")
+        result["ceiling"] = {"random_row_read_GBps": round(c1, 1), "rows_per_launch": nkeys,
+                             "frac_of_ceiling": round(achieved / c1, 4),
+                             "random_row_read_GBps_4x_rows": round(c4, 1),
+                             "frac_of_4x_rows_ceiling": round(achieved / c4, 4)}
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, d_table, batches[:4], bags, hot, rows, dim,
                                               args.cpu_seconds)

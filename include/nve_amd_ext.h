@@ -34,14 +34,15 @@ enum {
  * output_type: the value type's float precision (either precision for the
  * extension types).  split_hint: 0 lets the library choose how many lane
  * groups share a bag; > 0 forces that many (a power of two); < 0 forces one
- * group per bag (strict key order). */
+ * group per bag (strict key order).  unroll_hint: 0 lets the library choose how
+ * many row loads each lane group keeps in flight; 8 or 16 forces it. */
 NVE_C_API nve_status_t nve_amd_find_and_pool(
     nve_key_type_t key_type, int64_t num_keys, const void* keys, const void* table,
     int64_t num_rows, int64_t row_size_in_bytes, nve_data_type_t value_dtype,
     nve_pooling_type_t pooling_type, nve_sparse_type_t sparse_type, const void* csr_offsets,
     int64_t num_csr_offsets, int64_t fixed_hotness, const void* weights,
     nve_data_type_t weight_type, nve_data_type_t output_type, void* output,
-    int64_t output_stride, int32_t split_hint, void* stream);
+    int64_t output_stride, int32_t split_hint, int32_t unroll_hint, void* stream);
 
 /* Random-row read ceiling microbenchmark: reads row idx[i] (row_size_in_bytes
  * each, a multiple of 16) of a device table for i < n and folds the bytes into

@@ -634,7 +634,8 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
                                    int64_t num_csr_offsets, int64_t fixed_hotness,
                                    const void* weights, nve_data_type_t weight_type,
                                    nve_data_type_t output_type, void* output,
-                                   int64_t output_stride, int32_t split_hint, void* stream) {
+                                   int64_t output_stride, int32_t split_hint,
+                                   int32_t unroll_hint, void* stream) {
   C_TRY
   const int kb = key_bytes_of(key_type);
   const int vdt = dtype_in(value_dtype);
@@ -709,6 +710,9 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
   p.out_stride = output_stride;
   p.out_dtype = odt;
   p.force_split = split_hint;
+  NVE_CHECK_ARG(unroll_hint == 0 || unroll_hint == 8 || unroll_hint == 16,
+                "unroll_hint must be 0, 8 or 16");
+  p.force_unroll = unroll_hint;
   NVE_HIP(launch_pool(p, (hipStream_t)stream));
   return NVE_SUCCESS;
   C_CATCH

@@ -60,7 +60,8 @@ struct PoolLaunch {
   int64_t out_stride;
   int out_dtype;
   unsigned long long* miss_counter;
-  int force_split;  // 0: heuristic; > 0: groups per bag (power of two); < 0: one group per bag
+  int force_split;   // 0: heuristic; > 0: groups per bag (power of two); < 0: one group per bag
+  int force_unroll;  // 0: heuristic; 8 or 16: row loads in flight per lane group
 };
 
 hipError_t launch_gather(const GatherLaunch& a, hipStream_t stream);
@@ -75,7 +76,7 @@ hipError_t launch_read_ceiling(const uint8_t* table, uint64_t row_bytes, const i
 
 // Geometry the pool launcher picks (exposed for tests and the bench).
 struct PoolGeometry {
-  int vb, g, passes, gpb, threads, bags_per_wg;
+  int vb, g, passes, gpb, threads, bags_per_wg, unroll;
   int64_t grid;
   int lds_bytes;
 };

@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
 // ---------------------------------------------------------------------------
 // find-and-pool: one output row per bag
 // ---------------------------------------------------------------------------
-template <int SDT, int VB>
+template <int SDT, int VB, int U>
 __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, int gpb_shift,
                                                    int passes) {
   constexpr int ES = Fmt<SDT>::esize;
@@ -156,7 +156,8 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
 
   const bool weighted = a.weighted != 0;
   const int64_t value_bytes = a.count * ES;
-  const int out_es = (a.out_dtype == kF16) ? 2 : 4;
+  const bool out_f16 = a.out_dtype == kF16;
+  const int out_es = out_f16 ? 2 : 4;
   uint32_t misses = 0;
 
   for (int p = 0; p < passes; ++p) {
@@ -180,11 +181,11 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
         if (weighted) w = load_weight(a.weights, a.weight_dtype, kk);
       }
       const int n = (int)((ce - k0) < G ? (ce - k0) : G);
-      for (int j0 = 0; j0 < n; j0 += kUnroll) {
-        Vec<VB> v[kUnroll];
-        Meta m[kUnroll];
+      for (int j0 = 0; j0 < n; j0 += U) {
+        Vec<VB> v[U];
+        Meta m[U];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
           const int j = (j0 + u < n) ? j0 + u : n - 1;
           const uint64_t ra = shfl64(addr, gbase + j);
           if (j0 + u < n) {
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
           }
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
           if (j0 + u < n) {  // uniform over the group
             float wu = 1.0f;
             if (weighted) {
@@ -213,45 +214,100 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
       }
     }
 
-    bool owner = true;  // this group writes the bag's row
-    if (gpb > 1) {
-      float* red = lds;
-      float* wred = lds + (int64_t)blockDim.x * E;
-      const int slot = (grp * G + gl) * E;
+    if (gpb == 1) {
+      // one group per bag: the bag was reduced in key order
+      if (live && in_row) {
+        if (a.mean) {
+          const float d = weighted ? wsum : (float)(e - s);
 #pragma unroll
-      for (int c = 0; c < E; ++c) red[slot + c] = acc[c];
-      if (gl == 0) wred[grp] = wsum;
-      __syncthreads();
-      // Tree step st: chunk c < st adds chunk c + st.  Chunk c's slot is read
-      // in step st only by chunk c - st, which does not exist when c < st, so
-      // writing it back in the same step is race-free.
-      for (int st = gpb >> 1; st >= 1; st >>= 1) {
-        if (chunk < st) {
-          const int other = ((grp + st) * G + gl) * E;
-#pragma unroll
-          for (int c = 0; c < E; ++c) {
-            acc[c] += red[other + c];
-            red[slot + c] = acc[c];
-          }
-          wsum += wred[grp + st];
-          if (gl == 0) wred[grp] = wsum;
+          for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
         }
-        __syncthreads();
+        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride +
+                     ((int64_t)p * G + gl) * E * out_es;
+        store_out<E>(o, acc, out_f16);
       }
-      owner = (chunk == 0);
+      continue;
     }
 
-    if (owner && live && in_row) {
-      if (a.mean) {
-        const float d = weighted ? wsum : (float)(e - s);
+    // Split bag.  (1) Butterfly over the bag's groups inside the wave: step m
+    // pairs lane l with lane l ^ m, so after log2(span / G) steps every lane of
+    // the bag holds ((g0 + g1) + (g2 + g3)) ... (float addition is commutative,
+    // both partners compute the same bits).
+    const int span = gpb * G < 64 ? gpb * G : 64;
+    for (int mk = G; mk < span; mk <<= 1) {
 #pragma unroll
-        for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
-      }
-      uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride +
-                   ((int64_t)p * G + gl) * E * out_es;
-      store_out<E>(o, acc, a.out_dtype == kF16);
+      for (int c = 0; c < E; ++c) acc[c] += __shfl_xor(acc[c], mk);
+      wsum += __shfl_xor(wsum, mk);
     }
-    if (gpb > 1) __syncthreads();
+    if (gpb * G <= 64) {
+      if (chunk == 0 && live && in_row) {
+        if (a.mean) {
+          const float d = weighted ? wsum : (float)(e - s);
+#pragma unroll
+          for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
+        }
+        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride +
+                     ((int64_t)p * G + gl) * E * out_es;
+        store_out<E>(o, acc, out_f16);
+      }
+      continue;
+    }
+
+    // (2) The bag spans several waves: each wave's first group parks its
+    // partial row in LDS, then one thread per output element adds the waves'
+    // partials in wave order and writes the element.
+    const int row_elems = G * E;
+    const int wave = tid >> 6;
+    const int waves_per_bag = (gpb * G) >> 6;
+    float* red = lds;
+    float* wred = lds + (blockDim.x >> 6) * row_elems;
+    if ((tid & 63) < G) {
+#pragma unroll
+      for (int c = 0; c < E; ++c) red[wave * row_elems + gl * E + c] = acc[c];
+      if (gl == 0) wred[wave] = wsum;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < bags_per_wg * row_elems; idx += blockDim.x) {
+      const int b = idx / row_elems;
+      const int x = idx - b * row_elems;
+      const int64_t bg = (int64_t)blockIdx.x * bags_per_wg + b;
+      const bool elem_in_row = ((int64_t)p * G + x / E) * VB < value_bytes;
+      if (bg < a.num_bags && elem_in_row) {
+        const int w0 = b * waves_per_bag;
+        float v = red[w0 * row_elems + x];
+        float ws = wred[w0];
+        for (int w = 1; w < waves_per_bag; ++w) {
+          v += red[(w0 + w) * row_elems + x];
+          ws += wred[w0 + w];
+        }
+        if (a.mean) {
+          float d;
+          if (weighted) {
+            d = ws;
+          } else {
+            int64_t bs, be;
+            if (a.offsets != nullptr) {
+              bs = load_key(a.offsets, a.key_bytes, bg);
+              be = load_key(a.offsets, a.key_bytes, bg + 1);
+              bs = bs < 0 ? 0 : (bs > a.num_keys ? a.num_keys : bs);
+              be = be < bs ? bs : (be > a.num_keys ? a.num_keys : be);
+            } else {
+              bs = 0;
+              be = a.hotness;
+            }
+            d = (float)(be - bs);
+          }
+          v = (d == 0.0f) ? 0.0f : v / d;
+        }
+        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bg * a.out_stride +
+                     ((int64_t)p * row_elems + x) * out_es;
+        if (out_f16)
+          *reinterpret_cast<uint16_t*>(o) = f2h(v);
+        else
+          *reinterpret_cast<float*>(o) = v;
+      }
+    }
+    __syncthreads();
   }
   if (a.miss_counter != nullptr) add_misses(a.miss_counter, misses);
 }
@@ -456,7 +512,13 @@ bool pool_geometry(const PoolLaunch& a, PoolGeometry* g) {
   g->threads = threads;
   g->bags_per_wg = bags_per_wg;
   g->grid = (bags + bags_per_wg - 1) / bags_per_wg;
-  g->lds_bytes = gpb > 1 ? (int)(threads * (vb / esize) * 4 + (threads / G) * 4) : 0;
+  // LDS only when a bag spans several waves: one partial row + weight sum per wave
+  g->lds_bytes = gpb * G > 64 ? (int)((threads / 64) * (G * (vb / esize) * 4 + 4)) : 0;
+  // 16 row loads in flight per group only pay off when a group walks long
+  // key runs; 16-key chunks (the 1024-key bags of the benchmark over 64
+  // groups) measured slightly faster with 8
+  g->unroll = (avg / gpb) >= 32 ? 16 : 8;
+  if (a.force_unroll == 8 || a.force_unroll == 16) g->unroll = a.force_unroll;
   return true;
 }
 
@@ -467,7 +529,15 @@ hipError_t launch_pool(const PoolLaunch& a, hipStream_t stream) {
   if (g.grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const int gs = log2i(g.g);
   const int ps = log2i(g.gpb);
-#define L_POOL(S, V) hipLaunchKernelGGL((pool_kernel<S, V>), dim3(g.grid), dim3(g.threads), g.lds_bytes, stream, a, gs, ps, g.passes)
+#define L_POOL(S, V)                                                                        \
+  do {                                                                                      \
+    if (g.unroll == 16)                                                                     \
+      hipLaunchKernelGGL((pool_kernel<S, V, 16>), dim3(g.grid), dim3(g.threads), g.lds_bytes, \
+                         stream, a, gs, ps, g.passes);                                      \
+    else                                                                                    \
+      hipLaunchKernelGGL((pool_kernel<S, V, 8>), dim3(g.grid), dim3(g.threads), g.lds_bytes,  \
+                         stream, a, gs, ps, g.passes);                                      \
+  } while (0)
 #define P_F32(V) L_POOL(kF32, V)
 #define P_F16(V) L_POOL(kF16, V)
 #define P_QI8F32(V) L_POOL(kQI8F32, V)

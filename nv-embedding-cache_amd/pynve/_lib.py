@@ -140,7 +140,7 @@ SIGNATURES = {
     "nve_layer_get_num_tables": (I32, [P, PI64]),
     # extensions
     "nve_amd_find_and_pool": (I32, [ctypes.c_int, I64, P, P, I64, I64, I32, ctypes.c_int,
-                                    ctypes.c_int, P, I64, I64, P, I32, I32, P, I64, I32, P]),
+                                    ctypes.c_int, P, I64, I64, P, I32, I32, P, I64, I32, I32, P]),
     "nve_amd_read_ceiling": (I32, [P, I64, P, I64, P, P]),
     "nve_amd_gpu_table_num_sets": (I32, [P, PI64]),
     "nve_amd_gpu_table_export_state": (I32, [P, P, P, P, PI64]),

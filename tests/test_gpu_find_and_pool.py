@@ -23,12 +23,13 @@ CDT = {O.F32: _lib.DT_F32, O.F16: _lib.DT_F16, O.XI8A_F32: _lib.DT_XI8A_F32,
 
 
 def fap(d_keys, n, d_table, rows, width, vdt, pooling, sparse, d_off, n_off, hot, d_w, wdt, odt,
-        d_out, stride, split=0, key_type=_lib.KEY_INT64):
+        d_out, stride, split=0, key_type=_lib.KEY_INT64, unroll=0):
     _lib.call("nve_amd_find_and_pool", key_type, n, vp(d_keys), vp(d_table), rows, width, vdt, pooling,
-              sparse, vp(d_off), n_off, hot, vp(d_w), wdt, odt, vp(d_out), stride, split, stream_ptr())
+              sparse, vp(d_off), n_off, hot, vp(d_w), wdt, odt, vp(d_out), stride, split, unroll,
+              stream_ptr())
 
 
-def run_pool(tb, dtype, keys, pooling, sparse, off, bags, hot, w, wdt, out_dtype, split=0):
+def run_pool(tb, dtype, keys, pooling, sparse, off, bags, hot, w, wdt, out_dtype, split=0, unroll=0):
     rows, width = tb.shape
     count = (width - O.meta_bytes(dtype)) // O.value_bytes(dtype)
     oes = 2 if out_dtype == O.F16 else 4
@@ -36,20 +37,22 @@ def run_pool(tb, dtype, keys, pooling, sparse, off, bags, hot, w, wdt, out_dtype
     fap(to_dev(keys), keys.size, to_dev(tb.reshape(-1)), rows, width, CDT[dtype], pooling, sparse,
         None if off is None else to_dev(off), 0 if off is None else off.size, hot,
         None if w is None else to_dev(w), 0 if w is None else (_lib.DT_F16 if wdt == O.F16 else _lib.DT_F32),
-        CDT[out_dtype], out, count * oes, split)
+        CDT[out_dtype], out, count * oes, split, unroll=unroll)
     torch.cuda.synchronize()
     return out.cpu().numpy().view(np.uint16 if out_dtype == O.F16 else np.float32).reshape(bags, count)
 
 
-@pytest.mark.parametrize("split", [-1, 2, 8, 64])
-@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_WMEAN])
-def test_split_shapes_on_random_data(split, pooling):
+@pytest.mark.parametrize("split", [-1, 2, 4, 8, 16, 64])
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WMEAN])
+@pytest.mark.parametrize("unroll", [8, 16])
+def test_split_shapes_on_random_data(split, pooling, unroll):
     rng = np.random.default_rng(11 + split)
     rows, dim, bags, hot = 20000, 128, 48, 300
     tb = float_table(rng, rows, dim, O.F32, dyadic_values=False)
     keys = rng.integers(0, rows, size=bags * hot).astype(np.int64)
     w = rng.uniform(0, 1, size=keys.size).astype(np.float32) if pooling == _lib.POOL_WMEAN else None
-    got = run_pool(tb, O.F32, keys, pooling, _lib.SPARSE_FIXED, None, bags, hot, w, O.F32, O.F32, split)
+    got = run_pool(tb, O.F32, keys, pooling, _lib.SPARSE_FIXED, None, bags, hot, w, O.F32, O.F32, split,
+                   unroll)
     ref = oracle_pool(tb, keys, O.F32, dim, O.FIXED, pooling, None, bags, hot, w, O.F32, O.F32)
     if split == -1:
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))  # key order: bit-exact
