@@ -48,6 +48,7 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), (int64_t)ways, 0, nullptr));
   NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, nullptr));
   NVE_HIP(hipDeviceSynchronize());
+  build_decay_table();
 }
 
 GpuTable::~GpuTable() {
@@ -60,6 +61,7 @@ GpuTable::~GpuTable() {
   (void)hipFree(tags_);
   (void)hipFree(counters_);
   (void)hipFree(set_ts_);
+  (void)hipFree(decay_table_);
 }
 
 RowSource GpuTable::row_source(bool with_uvm) const {

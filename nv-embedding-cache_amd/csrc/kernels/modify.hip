@@ -1,0 +1,402 @@
+// modify.hip -- cache insert on the GPU: key histogram, per-set replacement
+// policy and the invalidate -> copy rows -> commit tags protocol.
+//
+// Reference behaviour restated (file:line in /root/reference):
+//   histogram   DefaultGPUHistogram::compute_histogram (gather_keys_data_ptrs.cuh:121-191):
+//               unique keys ordered by count descending, ties by ascending key
+//               (stable sorts), priority = float(count) * (1 / float(n)), row =
+//               backing table + key*row (insert_from_uvm) or values + first
+//               position*stride (insert)
+//   replacement SetReplaceDataKernel + SortBlock + MergeBlock
+//               (ec_set_associative_modify.cuh:36-309): per touched set, lazy
+//               decay of the 8 way counters by rate^(ts - set_ts), hits add
+//               their priority, misses compete 8 at a time through the bitonic
+//               networks, the best <= min(8, candidates) replace the ways of
+//               lowest counter (an empty way counts 0) when priority > counter
+//   protocol    CacheSADeviceModify::insert (ec_set_associative_device_modify.cuh:225-288):
+//               invalidate the replaced ways' tags, synchronize, copy the rows,
+//               write the new tags
+//
+// The replacement runs one 8-lane group per set (8 sets per wave); the way
+// counters live in the lanes' registers and the two bitonic networks are
+// shuffles inside the group, lane for lane the reference's networks (their tie
+// rules included), so the resulting residency is the same.  The decay factor
+// comes from a table of (float)pow((double)rate, (double)delta) built on the
+// host; the reference computes it with CUDA's __powf, whose bits are not
+// published.
+#include "device_common.cuh"
+#include "modify_launch.hpp"
+#include "sort_launch.hpp"
+
+namespace nve_amd {
+
+// sign-preserving map of a key to an unsigned sort key
+__device__ __forceinline__ uint64_t flip_key(int64_t k, int key_bytes) {
+  if (key_bytes == 4) return (uint64_t)((uint32_t)(int32_t)k ^ 0x80000000u);
+  return (uint64_t)k ^ 0x8000000000000000ull;
+}
+__device__ __forceinline__ int64_t unflip_key(uint64_t f, int key_bytes) {
+  if (key_bytes == 4) return (int64_t)(int32_t)((uint32_t)f ^ 0x80000000u);
+  return (int64_t)(f ^ 0x8000000000000000ull);
+}
+
+__global__ __launch_bounds__(256) void hist_prep_kernel(const void* keys, int key_bytes, int64_t n,
+                                                        uint64_t* k64, uint32_t* v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    k64[i] = flip_key(load_key(keys, key_bytes, i), key_bytes);
+    v[i] = (uint32_t)i;
+  }
+}
+
+// heads[i] = 1 where a run of equal sorted keys starts
+__global__ __launch_bounds__(256) void run_heads_kernel(const uint64_t* ks, int64_t n,
+                                                        uint32_t* heads) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) heads[i] = (i == 0 || ks[i] != ks[i - 1]) ? 1u : 0u;
+}
+
+// For each run u (start i): start[u] = i, key[u], first position[u]; start[U] = n.
+// heads was scanned in place (exclusive), flags recomputed from the keys.
+__global__ __launch_bounds__(256) void run_gather_kernel(const uint64_t* ks, const uint32_t* vs,
+                                                         const uint32_t* scan, int64_t n,
+                                                         uint32_t* start, uint64_t* ukey,
+                                                         uint32_t* first) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const bool head = (i == 0 || ks[i] != ks[i - 1]);
+  if (head) {
+    const uint32_t u = scan[i];
+    start[u] = (uint32_t)i;
+    ukey[u] = ks[i];
+    first[u] = vs[i];
+  }
+  if (i == n - 1) start[scan[i] + (head ? 1u : 0u)] = (uint32_t)n;
+}
+
+// count sort key: ascending order of (max_count - count) = count descending
+__global__ __launch_bounds__(256) void count_key_kernel(const uint32_t* start, uint32_t u_n,
+                                                        uint64_t* k2, uint32_t* v2) {
+  const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
+  if (u < u_n) {
+    const uint32_t c = start[u + 1] - start[u];
+    k2[u] = (uint64_t)(0xffffffffu - c);
+    v2[u] = u;
+  }
+}
+
+// Histogram entry h (hist order): key, priority, source row, and its set.
+__global__ __launch_bounds__(256) void hist_gather_kernel(
+    const uint32_t* order, const uint32_t* start, const uint64_t* ukey, const uint32_t* first,
+    uint32_t m, int key_bytes, float norm, const uint8_t* rows_base, int64_t row_stride,
+    int by_key, uint64_t num_sets, int64_t* hkeys, float* hprio, uint64_t* hsrc, uint64_t* k3,
+    uint32_t* v3) {
+  const uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= m) return;
+  const uint32_t u = order[h];
+  const int64_t key = unflip_key(ukey[u], key_bytes);
+  const uint32_t c = start[u + 1] - start[u];
+  hkeys[h] = key;
+  hprio[h] = (float)(int32_t)c * norm;
+  const int64_t idx = by_key ? key : (int64_t)first[u];
+  hsrc[h] = (uint64_t)rows_base + (uint64_t)idx * (uint64_t)row_stride;
+  const uint64_t set = key_bytes == 4 ? (uint64_t)((uint32_t)(int32_t)key % (uint32_t)num_sets)
+                                      : (uint64_t)key % num_sets;
+  k3[h] = set;
+  v3[h] = h;
+}
+
+// represented sets: rset[r], roff[r] (start in the set-sorted order), roff[R] = m
+__global__ __launch_bounds__(256) void set_gather_kernel(const uint64_t* ks, const uint32_t* scan,
+                                                         int64_t m, uint32_t* rset, uint32_t* roff) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const bool head = (i == 0 || ks[i] != ks[i - 1]);
+  if (head) {
+    rset[scan[i]] = (uint32_t)ks[i];
+    roff[scan[i]] = (uint32_t)i;
+  }
+  if (i == m - 1) roff[scan[i] + (head ? 1u : 0u)] = (uint32_t)m;
+}
+
+// ---------------------------------------------------------------------------
+// replacement: one 8-lane group per represented set
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float g8f(float v, int src) { return __shfl(v, src, 8); }
+__device__ __forceinline__ uint32_t g8u(uint32_t v, int src) {
+  return (uint32_t)__shfl((int)v, src, 8);
+}
+
+// SortBlock (ec_set_associative_modify.cuh:36-71): bitonic network over the 8
+// lanes, a lane swapping with its partner only when the values differ.
+__device__ __forceinline__ void sort_block8(float& v, uint32_t& pos, int x) {
+  for (int k = 2; k <= 8; k *= 2) {
+    for (int j = k / 2; j > 0; j /= 2) {
+      const int p = x ^ j;
+      const uint32_t pp = g8u(pos, p);
+      const float pv = g8f(v, p);
+      if (v != pv) {
+        const bool in_order_pos = x > p;
+        const bool in_order_val = v > pv;
+        const bool swap = (x & k) ? (in_order_pos != in_order_val) : (in_order_pos == in_order_val);
+        if (swap) {
+          pos = pp;
+          v = pv;
+        }
+      }
+    }
+  }
+}
+
+// MergeBlock (ec_set_associative_modify.cuh:73-103): take the partner-reversed
+// second list where strictly larger (its position passing through a float, as
+// in the reference), then a bitonic clean-up with no equality guard.
+__device__ __forceinline__ void merge_block8(float& p1, uint32_t& pos1, float p2, uint32_t pos2,
+                                             int x) {
+  const float rp = g8f(p2, 7 - x);
+  const float rpos = (float)g8u(pos2, 7 - x);
+  if (rp > p1) {
+    p1 = rp;
+    pos1 = (uint32_t)rpos;
+  }
+  for (int j = 4; j > 0; j /= 2) {
+    const int pr = x ^ j;
+    const uint32_t ppos = g8u(pos1, pr);
+    const float pp = g8f(p1, pr);
+    const bool in_order_pos = x < pr;
+    const bool in_order_p = p1 > pp;
+    if (in_order_pos != in_order_p) {
+      pos1 = ppos;
+      p1 = pp;
+    }
+  }
+}
+
+template <typename K, typename UK>
+__global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
+  const int x = threadIdx.x & 7;
+  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+  if (r >= a.num_rsets) return;  // whole 8-lane groups leave together
+  const uint32_t set = a.rset[r];
+  const uint32_t base = a.roff[r];
+  const uint32_t cnt = a.roff[r + 1] - base;
+  const K* tags = static_cast<const K*>(a.tags) + (uint64_t)set * 8;
+  float* ctr = a.counters + (uint64_t)set * 8;
+  const UK ns = (UK)a.num_sets;
+  const K sentinel = (K)a.sentinel;
+
+  // lazy decay of this lane's way counter, then stamp the set current
+  float c = ctr[x];
+  const int64_t delta = a.global_ts - a.set_ts[set];
+  if (delta > 0 && a.decay_rate != 1.0f) {
+    const float f = delta < a.decay_len ? a.decay_table[delta]
+                                        : (float)pow((double)a.decay_rate, (double)delta);
+    c *= f;
+  }
+  const K my_tag = tags[x];
+
+  float best = 0.0f;
+  uint32_t best_pos = 0;
+  for (uint32_t done = 0; done == 0 || done < cnt; done += 8) {
+    float hp = 0.0f;
+    uint32_t hpos = 0;
+    uint32_t hit_ways = 0;  // every way holding this candidate's key
+    float prio = 0.0f;
+    if (done + x < cnt) {
+      const uint32_t loc = a.order[base + done + x];
+      const K key = (K)a.hkeys[loc];
+      prio = a.hprio[loc];
+      for (int w = 0; w < 8; ++w) {
+        const K tw = tags[w];
+        if ((K)((UK)tw * ns + (UK)set) == key) hit_ways |= 1u << w;
+      }
+      if (hit_ways == 0) {
+        hpos = loc;
+        hp = prio;
+      }
+    }
+    // a way holds one key, so at most one candidate of the chunk adds to it
+    for (int sl = 0; sl < 8; ++sl) {
+      const uint32_t hw = g8u(hit_ways, sl);
+      const float hpr = g8f(prio, sl);
+      if ((hw >> x) & 1u) c += hpr;
+    }
+    sort_block8(hp, hpos, x);
+    if (done == 0) {
+      best = hp;
+      best_pos = hpos;
+    } else {
+      merge_block8(best, best_pos, hp, hpos, x);
+    }
+  }
+
+  // order the ways by counter (an empty way counts 0), reverse to ascending
+  float cv = (my_tag == sentinel) ? 0.0f : c;
+  uint32_t dpos = (uint32_t)x;
+  sort_block8(cv, dpos, x);
+  const uint32_t rd = g8u(dpos, 7 - x);
+  const float rc = g8f(cv, 7 - x);
+  const uint32_t num_repl = cnt < 8 ? cnt : 8;
+  const bool write = ((uint32_t)x < num_repl) && (best > rc);
+  if (write) {
+    const uint32_t slot = atomicAdd(a.num_records, 1u);
+    if (slot < a.max_records) {
+      const int64_t key = a.hkeys[best_pos];
+      a.rec_slot[slot] = (uint64_t)set * 8 + rd;
+      a.rec_tag[slot] = (int64_t)(K)((UK)(K)key / ns);  // embed_cache_construct_tag
+      a.rec_src[slot] = a.hsrc[best_pos];
+    }
+  }
+  // the replaced way's counter becomes the winner's priority
+  for (int sl = 0; sl < 8; ++sl) {
+    const int wr = __shfl((int)write, sl, 8);
+    const uint32_t wd = g8u(rd, sl);
+    const float wb = g8f(best, sl);
+    if (wr && wd == (uint32_t)x) c = wb;
+  }
+  ctr[x] = c;
+  if (x == 0) a.set_ts[set] = a.global_ts;
+}
+
+// ---------------------------------------------------------------------------
+// protocol kernels over the replacement records
+// ---------------------------------------------------------------------------
+template <typename K>
+__global__ __launch_bounds__(256) void invalidate_kernel(const uint32_t* num, uint32_t max_records,
+                                                         const uint64_t* slot, K* tags, K sentinel) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t n = *num < max_records ? *num : max_records;
+  if (i < n) tags[slot[i]] = sentinel;
+}
+
+template <typename K>
+__global__ __launch_bounds__(256) void commit_kernel(const uint32_t* num, uint32_t max_records,
+                                                     const uint64_t* slot, const int64_t* tag,
+                                                     K* tags) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t n = *num < max_records ? *num : max_records;
+  if (i < n) tags[slot[i]] = (K)tag[i];
+}
+
+// one wave per record: 16-byte (or 4 / 1 byte) chunks of the row
+template <int VB>
+__global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* num, uint32_t max_records,
+                                                        const uint64_t* slot, const uint64_t* src,
+                                                        uint8_t* data, uint64_t row_bytes) {
+  const int64_t rec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t n = *num < max_records ? *num : max_records;
+  if (rec >= n) return;
+  const uint8_t* s = reinterpret_cast<const uint8_t*>(src[rec]);
+  uint8_t* d = data + slot[rec] * row_bytes;
+  for (uint64_t o = (uint64_t)lane * VB; o < row_bytes; o += 64 * VB)
+    store_vec<VB>(d + o, load_vec<VB>(s + o));
+}
+
+// ---------------------------------------------------------------------------
+hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t* k64, uint32_t* v,
+                            hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(hist_prep_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, keys, key_bytes,
+                     n, k64, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(run_heads_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, n, heads);
+  return hipGetLastError();
+}
+
+hipError_t launch_run_gather(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan, int64_t n,
+                             uint32_t* start, uint64_t* ukey, uint32_t* first, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(run_gather_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, vs, scan, n,
+                     start, ukey, first);
+  return hipGetLastError();
+}
+
+hipError_t launch_count_key(const uint32_t* start, uint32_t u_n, uint64_t* k2, uint32_t* v2,
+                            hipStream_t stream) {
+  if (u_n == 0) return hipSuccess;
+  hipLaunchKernelGGL(count_key_kernel, dim3((u_n + 255) / 256), dim3(256), 0, stream, start, u_n, k2,
+                     v2);
+  return hipGetLastError();
+}
+
+hipError_t launch_hist_gather(const uint32_t* order, const uint32_t* start, const uint64_t* ukey,
+                              const uint32_t* first, uint32_t m, int key_bytes, float norm,
+                              const uint8_t* rows_base, int64_t row_stride, int by_key,
+                              uint64_t num_sets, int64_t* hkeys, float* hprio, uint64_t* hsrc,
+                              uint64_t* k3, uint32_t* v3, hipStream_t stream) {
+  if (m == 0) return hipSuccess;
+  hipLaunchKernelGGL(hist_gather_kernel, dim3((m + 255) / 256), dim3(256), 0, stream, order, start,
+                     ukey, first, m, key_bytes, norm, rows_base, row_stride, by_key, num_sets, hkeys,
+                     hprio, hsrc, k3, v3);
+  return hipGetLastError();
+}
+
+hipError_t launch_set_gather(const uint64_t* ks, const uint32_t* scan, int64_t m, uint32_t* rset,
+                             uint32_t* roff, hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(set_gather_kernel, dim3((m + 255) / 256), dim3(256), 0, stream, ks, scan, m, rset,
+                     roff);
+  return hipGetLastError();
+}
+
+hipError_t launch_set_replace(const ReplaceLaunch& a, int key_bytes, hipStream_t stream) {
+  if (a.num_rsets <= 0) return hipSuccess;
+  const int64_t threads = a.num_rsets * 8;
+  const int64_t grid = (threads + 255) / 256;
+  if (key_bytes == 4)
+    hipLaunchKernelGGL((set_replace_kernel<int32_t, uint32_t>), dim3(grid), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((set_replace_kernel<int64_t, uint64_t>), dim3(grid), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_invalidate(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                             void* tags, int key_bytes, int64_t sentinel, hipStream_t stream) {
+  if (max_records == 0) return hipSuccess;
+  const dim3 grid((max_records + 255) / 256);
+  if (key_bytes == 4)
+    hipLaunchKernelGGL(invalidate_kernel<int32_t>, grid, dim3(256), 0, stream, num, max_records, slot,
+                       (int32_t*)tags, (int32_t)sentinel);
+  else
+    hipLaunchKernelGGL(invalidate_kernel<int64_t>, grid, dim3(256), 0, stream, num, max_records, slot,
+                       (int64_t*)tags, (int64_t)sentinel);
+  return hipGetLastError();
+}
+
+hipError_t launch_commit(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                         const int64_t* tag, void* tags, int key_bytes, hipStream_t stream) {
+  if (max_records == 0) return hipSuccess;
+  const dim3 grid((max_records + 255) / 256);
+  if (key_bytes == 4)
+    hipLaunchKernelGGL(commit_kernel<int32_t>, grid, dim3(256), 0, stream, num, max_records, slot, tag,
+                       (int32_t*)tags);
+  else
+    hipLaunchKernelGGL(commit_kernel<int64_t>, grid, dim3(256), 0, stream, num, max_records, slot, tag,
+                       (int64_t*)tags);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_rows(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                            const uint64_t* src, int src_align, uint8_t* data, uint64_t row_bytes,
+                            hipStream_t stream) {
+  if (max_records == 0) return hipSuccess;
+  const dim3 grid(((uint64_t)max_records * 64 + 255) / 256);
+  const bool d16 = ((uintptr_t)data % 16 == 0) && row_bytes % 16 == 0;
+  if (d16 && src_align % 16 == 0)
+    hipLaunchKernelGGL(copy_rows_kernel<16>, grid, dim3(256), 0, stream, num, max_records, slot, src,
+                       data, row_bytes);
+  else if (row_bytes % 4 == 0 && (uintptr_t)data % 4 == 0 && src_align % 4 == 0)
+    hipLaunchKernelGGL(copy_rows_kernel<4>, grid, dim3(256), 0, stream, num, max_records, slot, src,
+                       data, row_bytes);
+  else
+    hipLaunchKernelGGL(copy_rows_kernel<1>, grid, dim3(256), 0, stream, num, max_records, slot, src,
+                       data, row_bytes);
+  return hipGetLastError();
+}
+
+}  // namespace nve_amd

@@ -1,0 +1,57 @@
+// modify_launch.hpp -- host launchers of the cache insert kernels (modify.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nve_amd {
+
+// Arguments of the per-set replacement kernel.
+struct ReplaceLaunch {
+  const uint32_t* rset;   // represented sets
+  const uint32_t* roff;   // num_rsets + 1 offsets into order
+  int64_t num_rsets;
+  const uint32_t* order;  // histogram indices grouped by set (ascending within a set)
+  const int64_t* hkeys;   // histogram keys
+  const float* hprio;     // histogram priorities
+  const uint64_t* hsrc;   // histogram source rows
+  const void* tags;       // num_sets*8 tags of the key type
+  float* counters;        // num_sets*8
+  int64_t* set_ts;        // num_sets
+  int64_t global_ts;
+  float decay_rate;
+  const float* decay_table;  // decay_table[d] = (float)pow(rate, d), d < decay_len
+  int64_t decay_len;
+  uint64_t num_sets;
+  int64_t sentinel;
+  uint32_t* num_records;     // atomic record counter (zeroed by the caller)
+  uint32_t max_records;
+  uint64_t* rec_slot;        // set*8 + way
+  int64_t* rec_tag;          // new tag
+  uint64_t* rec_src;         // source row address
+};
+
+hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t* k64, uint32_t* v,
+                            hipStream_t stream);
+hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream);
+hipError_t launch_run_gather(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan, int64_t n,
+                             uint32_t* start, uint64_t* ukey, uint32_t* first, hipStream_t stream);
+hipError_t launch_count_key(const uint32_t* start, uint32_t u_n, uint64_t* k2, uint32_t* v2,
+                            hipStream_t stream);
+hipError_t launch_hist_gather(const uint32_t* order, const uint32_t* start, const uint64_t* ukey,
+                              const uint32_t* first, uint32_t m, int key_bytes, float norm,
+                              const uint8_t* rows_base, int64_t row_stride, int by_key,
+                              uint64_t num_sets, int64_t* hkeys, float* hprio, uint64_t* hsrc,
+                              uint64_t* k3, uint32_t* v3, hipStream_t stream);
+hipError_t launch_set_gather(const uint64_t* ks, const uint32_t* scan, int64_t m, uint32_t* rset,
+                             uint32_t* roff, hipStream_t stream);
+hipError_t launch_set_replace(const ReplaceLaunch& a, int key_bytes, hipStream_t stream);
+hipError_t launch_invalidate(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                             void* tags, int key_bytes, int64_t sentinel, hipStream_t stream);
+hipError_t launch_commit(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                         const int64_t* tag, void* tags, int key_bytes, hipStream_t stream);
+hipError_t launch_copy_rows(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
+                            const uint64_t* src, int src_align, uint8_t* data, uint64_t row_bytes,
+                            hipStream_t stream);
+
+}  // namespace nve_amd

@@ -1,0 +1,27 @@
+// sort_launch.hpp -- stable radix sort, exclusive scan and key-span helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <utility>
+
+namespace nve_amd {
+
+// Bytes of temporary storage radix_sort_pairs needs for n pairs.
+size_t radix_sort_temp_bytes(int64_t n);
+
+// Stable ascending sort of (keys[i], vals[i]) on bits [begin_bit, end_bit) of
+// the keys (begin_bit a multiple of 8).  Ping-pongs between (keys, vals) and
+// (keys_alt, vals_alt); *result_in_alt says which pair holds the result.
+hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
+                            int64_t n, int begin_bit, int end_bit, void* temp, int* result_in_alt,
+                            hipStream_t stream);
+
+// In-place exclusive scan of m uint32 (total, if non-null, gets the sum).
+hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, hipStream_t stream);
+
+// *out |= OR over i of (keys[i] ^ keys[0]); *out must start at 0.
+hipError_t key_span(const uint64_t* keys, int64_t n, unsigned long long* out, hipStream_t stream);
+
+}  // namespace nve_amd

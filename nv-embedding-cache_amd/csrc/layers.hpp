@@ -158,8 +158,9 @@ class GpuTable {
   std::shared_mutex& uvm_mutex() { return uvm_mu_; }
 
  private:
-  void modify_insert(ExecutionContext& ctx, int64_t n, const void* d_keys, const uint8_t* values,
-                     int64_t value_stride, bool from_uvm);
+  void modify_insert(ExecutionContext& ctx, int64_t n, const void* keys, const uint8_t* rows,
+                     int64_t row_stride, bool from_uvm);
+  void build_decay_table();
   int key_bytes_;
   GPUTableConfig cfg_;
   uint64_t num_sets_ = 0;
@@ -168,6 +169,9 @@ class GpuTable {
   float* counters_ = nullptr;
   int64_t* set_ts_ = nullptr;
   int64_t global_ts_ = 0;
+  float decay_rate_ = 0.95f;  // EmbedCacheSA::CacheConfig default (ec_set_associative.h:120)
+  float* decay_table_ = nullptr;
+  int64_t decay_len_ = 0;
   std::mutex modify_mu_;        // one modify at a time
   std::shared_mutex uvm_mu_;    // lookups shared, modifies exclusive
 };
@@ -232,6 +236,8 @@ class LinearUVMEmbeddingLayer : public EmbeddingLayer {
   std::mutex collect_mu_;
   std::vector<uint8_t> collected_;  // keys gathered for the next insert
   int64_t collected_n_ = 0;
+  int64_t insert_wait_ = 0;                       // lookups to skip before the next collection
+  std::shared_ptr<std::atomic<bool>> in_flight_;  // an auto-insert task is running
 };
 
 }  // namespace nve_amd

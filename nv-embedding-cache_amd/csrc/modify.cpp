@@ -1,14 +1,211 @@
-// modify.cpp -- GpuTable insert (placeholder until the GPU modify kernels land).
+// modify.cpp -- GpuTable::insert / insert_from_uvm: the cache insert pipeline
+// on the modify stream.
+//
+//   keys -> (1) histogram: stable radix sort of the keys, run-length encode,
+//                stable sort of the runs by count descending, truncate to
+//                max_modify_size (gather_keys_data_ptrs.cuh:121-191,
+//                gpu_table.cu:416-576)
+//        -> (2) group by set: stable radix sort of (set, histogram index)
+//                (ec_set_associative_modify.cuh:364-513)
+//        -> (3) per-set replacement kernel -> records (slot, tag, source row)
+//        -> (4) invalidate the records' tags, drain the device, copy the rows,
+//                commit the tags (ec_set_associative_device_modify.cuh:225-288,
+//                :428-451)
+// The host reads three counts back (unique keys, represented sets, records),
+// where the reference also synchronizes (gather_keys_data_ptrs.cuh:168,
+// ec_set_associative_modify.cuh:489, ec_set_associative_device_modify.cuh:443).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "kernels/cache_launch.hpp"
+#include "kernels/modify_launch.hpp"
+#include "kernels/sort_launch.hpp"
 #include "layers.hpp"
 
 namespace nve_amd {
 
-void GpuTable::insert(ExecutionContext&, int64_t, const void*, int64_t, int64_t, const void*) {
-  NVE_NOT_IMPLEMENTED("GPU table insert is not available yet");
+namespace {
+
+int bits_for(uint64_t max_value) {
+  int b = 0;
+  while (b < 64 && (max_value >> b) != 0) ++b;
+  return b;
 }
 
-void GpuTable::insert_from_uvm(ExecutionContext&, int64_t, const void*) {
-  NVE_NOT_IMPLEMENTED("GPU table insert is not available yet");
+int round8(int bits) { return (bits + 7) / 8 * 8; }
+
+template <typename T>
+T* carve(uint8_t*& p, size_t count) {
+  T* r = reinterpret_cast<T*>(p);
+  p += (count * sizeof(T) + 255) / 256 * 256;
+  return r;
+}
+
+uint32_t read_u32(const uint32_t* d, hipStream_t s) {
+  uint32_t h = 0;
+  NVE_HIP(hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  return h;
+}
+
+}  // namespace
+
+// Decay factors (float)pow((double)rate, (double)d) for d < len; the table
+// ends where the factor has become 0 in float (every larger d is 0 too) or at
+// 1M entries, beyond which the kernel evaluates pow itself.
+void GpuTable::build_decay_table() {
+  std::vector<float> t;
+  t.push_back(1.0f);
+  if (decay_rate_ < 1.0f) {
+    for (int64_t d = 1; d < (1 << 20); ++d) {
+      const float f = (float)std::pow((double)decay_rate_, (double)d);
+      t.push_back(f);
+      if (f == 0.0f) break;
+    }
+  }
+  decay_len_ = (int64_t)t.size();
+  NVE_HIP(hipMalloc((void**)&decay_table_, t.size() * sizeof(float)));
+  NVE_HIP(hipMemcpy(decay_table_, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice));
+}
+
+void GpuTable::insert(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+                      int64_t value_size, const void* values) {
+  ScopedDevice sd(cfg_.device_id);
+  if (n <= 0) return;
+  NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
+  NVE_CHECK(values != nullptr, "Invalid cache insert params");
+  NVE_CHECK(value_size == cfg_.row_size_in_bytes, "Unsupported value_size");
+  NVE_CHECK_ARG(value_stride >= value_size, "value_stride is smaller than value_size");
+  const hipStream_t stream = ctx.modify_stream();
+  const void* d_vals = device_input(ctx, "insert_values", values,
+                                    (size_t)(n - 1) * value_stride + value_size, stream);
+  modify_insert(ctx, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
+}
+
+void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* keys) {
+  ScopedDevice sd(cfg_.device_id);
+  NVE_CHECK(cfg_.uvm_table != nullptr, "insert_from_uvm requires a UVM table");
+  if (n <= 0) return;
+  NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
+  modify_insert(ctx, n, keys, static_cast<const uint8_t*>(cfg_.uvm_table), cfg_.row_size_in_bytes,
+                true);
+}
+
+void GpuTable::modify_insert(ExecutionContext& ctx, int64_t n, const void* keys,
+                             const uint8_t* rows, int64_t row_stride, bool from_uvm) {
+  NVE_CHECK(n <= (int64_t)UINT32_MAX, "Too many keys for one insert");
+  std::lock_guard<std::mutex> mk(modify_mu_);
+  const hipStream_t s = ctx.modify_stream();
+  const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, s);
+
+  // ---- scratch (grow-only, per context) ----
+  const size_t un = (size_t)n;
+  const size_t bytes = 16 * 256 + un * (8 * 2 + 4 * 2) * 3 + un * (4 * 4 + 8 * 4) +
+                       radix_sort_temp_bytes(n) + 64 * 256;
+  uint8_t* p = static_cast<uint8_t*>(ctx.buffer("insert_scratch", bytes));
+  unsigned long long* d_span = carve<unsigned long long>(p, 1);
+  uint32_t* d_count = carve<uint32_t>(p, 4);
+  uint64_t* ka = carve<uint64_t>(p, un);
+  uint32_t* va = carve<uint32_t>(p, un);
+  uint64_t* kb = carve<uint64_t>(p, un);
+  uint32_t* vb = carve<uint32_t>(p, un);
+  uint32_t* heads = carve<uint32_t>(p, un);
+  uint32_t* start = carve<uint32_t>(p, un + 1);
+  uint64_t* ukey = carve<uint64_t>(p, un);
+  uint32_t* first = carve<uint32_t>(p, un);
+  int64_t* hkeys = carve<int64_t>(p, un);
+  float* hprio = carve<float>(p, un);
+  uint64_t* hsrc = carve<uint64_t>(p, un);
+  uint32_t* rset = carve<uint32_t>(p, un);
+  uint32_t* roff = carve<uint32_t>(p, un + 1);
+  uint64_t* rec_slot = carve<uint64_t>(p, un);
+  int64_t* rec_tag = carve<int64_t>(p, un);
+  uint64_t* rec_src = carve<uint64_t>(p, un);
+  void* sort_tmp = carve<uint8_t>(p, radix_sort_temp_bytes(n));
+
+  // ---- (1) histogram ----
+  NVE_HIP(launch_hist_prep(d_keys, key_bytes_, n, ka, va, s));
+  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(d_span), 1, 0, s));
+  NVE_HIP(key_span(ka, n, d_span, s));
+  unsigned long long span = 0;
+  NVE_HIP(hipMemcpyAsync(&span, d_span, sizeof(span), hipMemcpyDeviceToHost, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  int alt = 0;
+  NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, round8(bits_for(span)), sort_tmp, &alt, s));
+  uint64_t* ks = alt ? kb : ka;
+  uint32_t* vs = alt ? vb : va;
+  NVE_HIP(launch_run_heads(ks, n, heads, s));
+  NVE_HIP(exclusive_scan_u32(heads, n, d_count, s));
+  const uint32_t uniq = read_u32(d_count, s);
+  NVE_HIP(launch_run_gather(ks, vs, heads, n, start, ukey, first, s));
+  // sort the runs by count descending (stable: ties keep ascending key order)
+  uint64_t* k2 = alt ? ka : kb;  // the buffers not holding ks / vs
+  uint32_t* v2 = alt ? va : vb;
+  uint64_t* k2b = reinterpret_cast<uint64_t*>(rec_slot);
+  uint32_t* v2b = reinterpret_cast<uint32_t*>(rset);
+  NVE_HIP(launch_count_key(start, uniq, k2, v2, s));
+  int alt2 = 0;
+  NVE_HIP(radix_sort_pairs(k2, v2, k2b, v2b, uniq, 0, round8(bits_for((uint64_t)n)), sort_tmp, &alt2, s));
+  const uint32_t* order = alt2 ? v2b : v2;
+  const uint32_t m = (uint32_t)std::min<int64_t>(uniq, cfg_.max_modify_size);
+  // hist entries and their sets (k3 / v3 reuse the first sort's free buffers)
+  uint64_t* k3 = alt ? kb : ka;
+  uint32_t* v3 = alt ? vb : va;
+  NVE_HIP(launch_hist_gather(order, start, ukey, first, m, key_bytes_, 1.0f / (float)n, rows,
+                             row_stride, from_uvm ? 1 : 0, num_sets_, hkeys, hprio, hsrc, k3, v3, s));
+
+  // ---- (2) group by set ----
+  uint64_t* k3b = reinterpret_cast<uint64_t*>(ukey);  // runs' keys are consumed by now
+  uint32_t* v3b = heads;
+  int alt3 = 0;
+  NVE_HIP(radix_sort_pairs(k3, v3, k3b, v3b, m, 0, round8(bits_for(num_sets_ - 1)), sort_tmp, &alt3, s));
+  const uint64_t* sk = alt3 ? k3b : k3;
+  const uint32_t* sv = alt3 ? v3b : v3;
+  NVE_HIP(launch_run_heads(sk, m, start, s));  // start reused as head flags
+  NVE_HIP(exclusive_scan_u32(start, m, d_count, s));
+  const uint32_t nrs = read_u32(d_count, s);
+  NVE_HIP(launch_set_gather(sk, start, m, rset, roff, s));
+
+  // ---- (3) replacement ----
+  ++global_ts_;  // once per insert (ec_set_associative_device_modify.cuh:262)
+  NVE_HIP(launch_fill_u32(d_count + 1, 1, 0, s));
+  ReplaceLaunch r{};
+  r.rset = rset;
+  r.roff = roff;
+  r.num_rsets = nrs;
+  r.order = sv;
+  r.hkeys = hkeys;
+  r.hprio = hprio;
+  r.hsrc = hsrc;
+  r.tags = tags_;
+  r.counters = counters_;
+  r.set_ts = set_ts_;
+  r.global_ts = global_ts_;
+  r.decay_rate = decay_rate_;
+  r.decay_table = decay_table_;
+  r.decay_len = decay_len_;
+  r.num_sets = num_sets_;
+  r.sentinel = cfg_.invalid_key;
+  r.num_records = d_count + 1;
+  r.max_records = m;
+  r.rec_slot = rec_slot;
+  r.rec_tag = rec_tag;
+  r.rec_src = rec_src;
+  NVE_HIP(launch_set_replace(r, key_bytes_, s));
+
+  // ---- (4) invalidate -> drain -> copy -> commit ----
+  NVE_HIP(launch_invalidate(d_count + 1, m, rec_slot, tags_, key_bytes_, cfg_.invalid_key, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  // lookups already queued on other streams may still read the old rows of
+  // the invalidated ways: let them finish before the rows are overwritten
+  NVE_HIP(hipDeviceSynchronize());
+  uintptr_t align = (uintptr_t)rows | (uintptr_t)row_stride;
+  const int src_align = (align % 16 == 0) ? 16 : (align % 4 == 0) ? 4 : 1;
+  NVE_HIP(launch_copy_rows(d_count + 1, m, rec_slot, rec_src, src_align, data_,
+                           (uint64_t)cfg_.row_size_in_bytes, s));
+  NVE_HIP(launch_commit(d_count + 1, m, rec_slot, rec_tag, tags_, key_bytes_, s));
+  NVE_HIP(hipStreamSynchronize(s));
 }
 
 }  // namespace nve_amd

@@ -122,6 +122,7 @@ ExecutionContext::~ExecutionContext() {
 }
 
 void* ExecutionContext::buffer(const std::string& name, size_t bytes, bool host) {
+  std::lock_guard<std::mutex> lk(bufs_mu_);
   Buf& b = bufs_[name];
   if (b.ptr && (b.bytes < bytes || b.host != host)) {
     // the stream may still use the old buffer

@@ -137,6 +137,7 @@ class ExecutionContext {
   int device_;
   hipStream_t lookup_, modify_;
   std::shared_ptr<ThreadPool> pool_;
+  std::mutex bufs_mu_;  // the lookup thread and a pool task (auto-insert) share buffers
   std::map<std::string, Buf> bufs_;
   unsigned long long* misses_ = nullptr;
   std::mutex pending_mu_;

@@ -111,8 +111,14 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
                                           float hitrate) {
   std::unique_lock<std::mutex> lk(collect_mu_, std::try_to_lock);
   if (!lk.owns_lock()) return;  // an insert is being collected or launched elsewhere
+  if (in_flight_ && in_flight_->load()) return;  // the previous insert still runs
   const int64_t min_size = cfg_.min_insert_size_gpu > 0 ? cfg_.min_insert_size_gpu : 1;
-  if (collected_n_ == 0 && !cfg_.insert_heuristic->insert_needed(hitrate, 0)) return;
+  if (collected_n_ == 0) {
+    // min_insert_freq_gpu lookups pass between inserts (layer_utils.cpp:120-131)
+    if (--insert_wait_ >= 0) return;
+    insert_wait_ = 0;
+    if (!cfg_.insert_heuristic->insert_needed(hitrate, 0)) return;
+  }
   const int64_t total = collected_n_ == 0 ? std::max(n, min_size) : min_size;
   const int64_t part = std::min(n, total - collected_n_);
   if (part <= 0) return;
@@ -127,9 +133,17 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
   const int64_t nk = collected_n_;
   collected_n_ = 0;
   // the insert itself runs as a pool task; wait() on the context joins it
+  insert_wait_ = cfg_.min_insert_freq_gpu;
+  if (!in_flight_) in_flight_ = std::make_shared<std::atomic<bool>>(false);
+  in_flight_->store(true);
   std::shared_ptr<GpuTable> table = table_;
+  std::shared_ptr<std::atomic<bool>> flag = in_flight_;
   ExecutionContext* c = &ctx;
-  ctx.add_pending(ctx.pool().submit([table, c, nk, keys = std::move(keys)]() {
+  ctx.add_pending(ctx.pool().submit([table, c, nk, flag, keys = std::move(keys)]() {
+    struct Done {
+      std::atomic<bool>* f;
+      ~Done() { f->store(false); }
+    } done{flag.get()};
     table->insert_from_uvm(*c, nk, keys.data());
   }));
 }

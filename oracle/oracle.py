@@ -250,6 +250,10 @@ class Cache:
         n = self.c.num_sets * 8
         return np.ctypeslib.as_array(ctypes.cast(self.c.counters, ctypes.POINTER(ctypes.c_float)), (n,)).copy()
 
+    def set_ts(self):
+        n = self.c.num_sets
+        return np.ctypeslib.as_array(ctypes.cast(self.c.set_ts, ctypes.POINTER(ctypes.c_int64)), (n,)).copy()
+
     def data(self):
         n = self.c.num_sets * 8 * self.row_bytes
         return np.ctypeslib.as_array(ctypes.cast(self.c.data, ctypes.POINTER(ctypes.c_uint8)), (n,))
