@@ -44,6 +44,29 @@ NVE_C_API nve_status_t nve_amd_find_and_pool(
     nve_data_type_t weight_type, nve_data_type_t output_type, void* output,
     int64_t output_stride, int32_t split_hint, int32_t unroll_hint, void* stream);
 
+/* Key dedup (the reference's Deduper::dedup, cuda_ops/deduper.cuh:136-221),
+ * device buffers of the key type, each sized num_keys: unique_out (ascending,
+ * signed order), counts_out, inverse_out (original positions ordered by key,
+ * stable: inverse_out[offsets_out[u] + j] is the j-th position of unique key
+ * u) and offsets_out (exclusive scan of the counts).  *num_unique receives the
+ * number of unique keys (the call synchronizes the stream).  workspace: device
+ * memory of nve_amd_dedup_workspace_size(num_keys) bytes. */
+NVE_C_API nve_status_t nve_amd_dedup_workspace_size(int64_t num_keys, uint64_t* bytes);
+NVE_C_API nve_status_t nve_amd_dedup(nve_key_type_t key_type, int64_t num_keys, const void* keys,
+                                     void* unique_out, void* counts_out, void* inverse_out,
+                                     void* offsets_out, int64_t* num_unique, void* workspace,
+                                     uint64_t workspace_bytes, void* stream);
+
+/* Dedup-then-gather over a linear table in device memory: output row i =
+ * table row keys[i], the keys read in sorted order so each distinct row is
+ * fetched once per run.  Keys outside [0, num_rows) leave their output row
+ * unchanged.  Asynchronous; workspace as for nve_amd_dedup. */
+NVE_C_API nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num_keys,
+                                            const void* keys, const void* table, int64_t num_rows,
+                                            int64_t row_size_in_bytes, void* output,
+                                            int64_t output_stride, void* workspace,
+                                            uint64_t workspace_bytes, void* stream);
+
 /* Random-row read ceiling microbenchmark: reads row idx[i] (row_size_in_bytes
  * each, a multiple of 16) of a device table for i < n and folds the bytes into
  * sink (one uint32 per 256-thread workgroup, ceil(n/128) words). */

@@ -8,6 +8,7 @@
 #include <new>
 
 #include "../../include/nve_amd_ext.h"
+#include "dedup.hpp"
 #include "layers.hpp"
 
 using namespace nve_amd;
@@ -714,6 +715,45 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
                 "unroll_hint must be 0, 8 or 16");
   p.force_unroll = unroll_hint;
   NVE_HIP(launch_pool(p, (hipStream_t)stream));
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_dedup_workspace_size(int64_t num_keys, uint64_t* bytes) {
+  if (!bytes) return set_error(NVE_ERROR_INVALID_ARGUMENT, "bytes must not be NULL");
+  if (num_keys < 0) return set_error(NVE_ERROR_INVALID_ARGUMENT, "Invalid num_keys");
+  *bytes = dedup_workspace_bytes(num_keys);
+  return NVE_SUCCESS;
+}
+
+nve_status_t nve_amd_dedup(nve_key_type_t key_type, int64_t num_keys, const void* keys,
+                           void* unique_out, void* counts_out, void* inverse_out, void* offsets_out,
+                           int64_t* num_unique, void* workspace, uint64_t workspace_bytes,
+                           void* stream) {
+  C_TRY
+  NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
+  NVE_CHECK_ARG(num_unique != nullptr, "num_unique must not be NULL");
+  if (num_keys > 0)
+    NVE_CHECK_ARG(keys && unique_out && counts_out && inverse_out && offsets_out,
+                  "keys and output buffers must not be NULL");
+  *num_unique = dedup_run(key_bytes_of(key_type), num_keys, keys, unique_out, counts_out,
+                          inverse_out, offsets_out, workspace, workspace_bytes, (hipStream_t)stream);
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num_keys, const void* keys,
+                                  const void* table, int64_t num_rows, int64_t row_size_in_bytes,
+                                  void* output, int64_t output_stride, void* workspace,
+                                  uint64_t workspace_bytes, void* stream) {
+  C_TRY
+  NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
+  NVE_CHECK_ARG(num_rows > 0 && row_size_in_bytes > 0, "Invalid table shape");
+  NVE_CHECK_ARG(output_stride >= row_size_in_bytes, "output_stride is smaller than a row");
+  if (num_keys > 0) NVE_CHECK_ARG(keys && table && output, "keys, table and output must not be NULL");
+  dedup_gather_run(key_bytes_of(key_type), num_keys, keys, static_cast<const uint8_t*>(table),
+                   num_rows, row_size_in_bytes, output, output_stride, workspace, workspace_bytes,
+                   (hipStream_t)stream);
   return NVE_SUCCESS;
   C_CATCH
 }

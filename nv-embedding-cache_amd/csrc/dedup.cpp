@@ -1,0 +1,119 @@
+// dedup.cpp -- host orchestration of key dedup (Deduper::dedup,
+// deduper.cuh:136-221) and of the dedup-ordered gather (dedup, then one table
+// read per distinct key run, UnpackDedup, cuda_utils.cuh:24-79, fused into it).
+#include "dedup.hpp"
+
+#include "kernels/cache_launch.hpp"
+#include "kernels/dedup_launch.hpp"
+#include "kernels/launch.hpp"
+#include "kernels/modify_launch.hpp"
+#include "kernels/sort_launch.hpp"
+#include "runtime.hpp"
+
+namespace nve_amd {
+
+namespace {
+
+int bits_for(uint64_t max_value) {
+  int b = 0;
+  while (b < 64 && (max_value >> b) != 0) ++b;
+  return b;
+}
+
+struct DedupBufs {
+  unsigned long long* span;
+  uint32_t* total;
+  uint64_t *ka, *kb;
+  uint32_t *va, *vb, *heads, *start;
+  void* sort_tmp;
+};
+
+size_t pad(size_t b) { return (b + 255) / 256 * 256; }
+
+DedupBufs carve(void* ws, int64_t n) {
+  uint8_t* p = static_cast<uint8_t*>(ws);
+  DedupBufs d;
+  d.span = reinterpret_cast<unsigned long long*>(p);
+  p += 256;
+  d.total = reinterpret_cast<uint32_t*>(p);
+  p += 256;
+  d.ka = reinterpret_cast<uint64_t*>(p);
+  p += pad(8 * n);
+  d.kb = reinterpret_cast<uint64_t*>(p);
+  p += pad(8 * n);
+  d.va = reinterpret_cast<uint32_t*>(p);
+  p += pad(4 * n);
+  d.vb = reinterpret_cast<uint32_t*>(p);
+  p += pad(4 * n);
+  d.heads = reinterpret_cast<uint32_t*>(p);
+  p += pad(4 * n);
+  d.start = reinterpret_cast<uint32_t*>(p);
+  p += pad(4 * (n + 1));
+  d.sort_tmp = p;
+  return d;
+}
+
+}  // namespace
+
+size_t dedup_workspace_bytes(int64_t n) {
+  if (n < 1) n = 1;
+  return 512 + 2 * pad(8 * n) + 4 * pad(4 * n) + pad(4 * (n + 1)) + radix_sort_temp_bytes(n);
+}
+
+int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
+                  void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (n <= 0) return 0;
+  NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
+  NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
+  DedupBufs b = carve(ws, n);
+  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, s));
+  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(b.span), 1, 0, s));
+  NVE_HIP(key_span(b.ka, n, b.span, s));
+  unsigned long long span = 0;
+  NVE_HIP(hipMemcpyAsync(&span, b.span, sizeof(span), hipMemcpyDeviceToHost, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  int alt = 0;
+  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, (bits_for(span) + 7) / 8 * 8, b.sort_tmp,
+                           &alt, s));
+  const uint64_t* ks = alt ? b.kb : b.ka;
+  const uint32_t* vs = alt ? b.vb : b.va;
+  NVE_HIP(launch_run_heads(ks, n, b.heads, s));
+  NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, s));
+  NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, s));
+  uint32_t u = 0;
+  NVE_HIP(hipMemcpyAsync(&u, b.total, sizeof(u), hipMemcpyDeviceToHost, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  NVE_HIP(launch_dedup_counts(b.start, u, key_bytes, counts, s));
+  return (int64_t)u;
+}
+
+void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t* table,
+                      int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride, void* ws,
+                      size_t ws_bytes, hipStream_t s) {
+  if (n <= 0) return;
+  NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
+  NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
+  DedupBufs b = carve(ws, n);
+  // rows of [0, num_rows): sort on the row-index bits only (keys outside the
+  // table stay unresolved and their output rows untouched)
+  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, s));
+  int alt = 0;
+  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0,
+                           (bits_for((uint64_t)(num_rows > 1 ? num_rows - 1 : 1)) + 7) / 8 * 8,
+                           b.sort_tmp, &alt, s));
+  GatherLaunch g{};
+  g.keys = alt ? b.kb : b.ka;  // sorted keys as int64
+  g.key_bytes = 8;
+  g.n = n;
+  g.src.table = table;
+  g.src.row_bytes = (uint64_t)row_bytes;
+  g.src.load_indices = 1;
+  g.src.num_rows = (uint64_t)num_rows;
+  g.raw = 1;
+  g.out = out;
+  g.out_stride = out_stride;
+  g.out_index = alt ? b.vb : b.va;  // original positions in key order
+  NVE_HIP(launch_gather(g, s));
+}
+
+}  // namespace nve_amd

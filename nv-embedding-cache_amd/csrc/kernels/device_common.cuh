@@ -275,6 +275,24 @@ __device__ __forceinline__ int64_t load_key(const void* keys, int key_bytes, int
                         : reinterpret_cast<const int64_t*>(keys)[i];
 }
 
+__device__ __forceinline__ void store_key(void* keys, int key_bytes, int64_t i, int64_t v) {
+  if (key_bytes == 4)
+    reinterpret_cast<int32_t*>(keys)[i] = (int32_t)v;
+  else
+    reinterpret_cast<int64_t*>(keys)[i] = v;
+}
+
+// Order-preserving map of a signed key to an unsigned radix-sort key (the
+// sign bit flipped), and back.
+__device__ __forceinline__ uint64_t flip_key(int64_t k, int key_bytes) {
+  if (key_bytes == 4) return (uint64_t)((uint32_t)(int32_t)k ^ 0x80000000u);
+  return (uint64_t)k ^ 0x8000000000000000ull;
+}
+__device__ __forceinline__ int64_t unflip_key(uint64_t f, int key_bytes) {
+  if (key_bytes == 4) return (int64_t)(int32_t)((uint32_t)f ^ 0x80000000u);
+  return (int64_t)(f ^ 0x8000000000000000ull);
+}
+
 // Where rows come from (RowSource, launch.hpp).  Without a cache: row =
 // table + index*row_bytes, index being the key (load_indices) or the key's
 // position (a buffer gathered earlier).  With a cache (EmbedCacheSA layout,
@@ -290,6 +308,7 @@ __device__ __forceinline__ uint64_t resolve_row(const RowSource& src, int key_by
   *miss = false;
   if (src.cache_data == nullptr) {
     const uint64_t idx = src.load_indices ? (uint64_t)key : (uint64_t)pos;
+    if (src.num_rows != 0 && idx >= src.num_rows) return 0;
     return (uint64_t)src.table + idx * src.row_bytes;
   }
   uint32_t set;

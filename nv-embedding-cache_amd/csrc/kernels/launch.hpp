@@ -19,6 +19,7 @@ struct RowSource {
   const uint8_t* cache_data; // null: no cache
   const void* cache_tags;    // num_sets*8 tags of the key type
   uint64_t num_sets;
+  uint64_t num_rows;         // linear table only: keys >= num_rows stay unresolved (0 = no bound)
 };
 
 // One output row per key: the raw stored row (raw != 0) or its dequantized
@@ -37,6 +38,7 @@ struct GatherLaunch {
   int out_dtype;
   uint64_t* hitmask;
   unsigned long long* miss_counter;  // optional: += number of cache misses
+  const uint32_t* out_index;         // optional: key i is written to output row out_index[i]
 };
 
 // One output row per bag (Fixed hotness or CSR offsets of the key type),

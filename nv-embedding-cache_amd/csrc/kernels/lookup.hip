@@ -59,9 +59,11 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
   }
   uint64_t addr = 0;
   bool miss = false;
+  uint32_t orow = (uint32_t)i;  // output row of this key
   if (valid && !skip) {
     const int64_t key = a.src.load_indices ? load_key(a.keys, a.key_bytes, i) : i;
     addr = resolve_row(a.src, a.key_bytes, key, i, &miss);
+    if (a.out_index != nullptr) orow = a.out_index[i];
   }
   if (a.hitmask != nullptr) {
     const uint64_t hits = __ballot(addr != 0);
@@ -84,11 +86,13 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
       Vec<VB> v[kUnroll];
       Meta m[kUnroll];
       uint64_t ra[kUnroll];
+      uint32_t orw[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int q = q0 + u;
         const int j = grp + (q < G ? q : 0) * groups;
         ra[u] = shfl64(addr, j);
+        orw[u] = a.out_index != nullptr ? shfl32(orow, j) : 0u;
         if (q >= G) ra[u] = 0;
         if (ra[u] != 0 && in_row) v[u] = load_vec<VB>(reinterpret_cast<const uint8_t*>(ra[u]) + off);
         if constexpr (!RAW && Fmt<SDT>::meta != 0) {
@@ -98,7 +102,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         if (ra[u] == 0 || !in_row) continue;
-        const int64_t row = tile * 64 + grp + (int64_t)(q0 + u) * groups;
+        const int64_t row = a.out_index != nullptr ? (int64_t)orw[u]
+                                                   : tile * 64 + grp + (int64_t)(q0 + u) * groups;
         uint8_t* o = out + row * a.out_stride;
         if constexpr (RAW) {
           store_vec<VB>(o + off, v[u]);

@@ -30,16 +30,6 @@
 
 namespace nve_amd {
 
-// sign-preserving map of a key to an unsigned sort key
-__device__ __forceinline__ uint64_t flip_key(int64_t k, int key_bytes) {
-  if (key_bytes == 4) return (uint64_t)((uint32_t)(int32_t)k ^ 0x80000000u);
-  return (uint64_t)k ^ 0x8000000000000000ull;
-}
-__device__ __forceinline__ int64_t unflip_key(uint64_t f, int key_bytes) {
-  if (key_bytes == 4) return (int64_t)(int32_t)((uint32_t)f ^ 0x80000000u);
-  return (int64_t)(f ^ 0x8000000000000000ull);
-}
-
 __global__ __launch_bounds__(256) void hist_prep_kernel(const void* keys, int key_bytes, int64_t n,
                                                         uint64_t* k64, uint32_t* v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -1,0 +1,108 @@
+"""GPU parity of key dedup (Deduper::dedup, cuda_ops/deduper.cuh:136-221) and
+of the dedup-then-gather of the C2 workload against the oracle.
+
+Cases follow tests/kernels/deduper_tests.cu:139-348: all unique, all
+identical, empty, single key, negative keys (signed order), random keys
+checked for the round-trip invariants, plus the benchmark's 262,144 Zipf keys.
+The gathered output must equal the plain gather bitwise."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from nve_helpers import float_table, stream_ptr, to_dev, vp
+from oracle import oracle as O
+from pynve import _lib
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def workspace(n):
+    b = ctypes.c_uint64()
+    _lib.call("nve_amd_dedup_workspace_size", n, ctypes.byref(b))
+    return torch.empty(max(int(b.value), 1), dtype=torch.uint8, device="cuda"), int(b.value)
+
+
+def gpu_dedup(keys):
+    n = keys.size
+    kt = _lib.KEY_INT32 if keys.dtype == np.int32 else _lib.KEY_INT64
+    tdt = torch.int32 if keys.dtype == np.int32 else torch.int64
+    d_keys = to_dev(keys) if n else torch.empty(1, dtype=tdt, device="cuda")
+    outs = [torch.full((max(n, 1),), -7, dtype=tdt, device="cuda") for _ in range(4)]
+    ws, wb = workspace(n)
+    nu = ctypes.c_int64(-1)
+    _lib.call("nve_amd_dedup", kt, n, vp(d_keys), *[vp(o) for o in outs], ctypes.byref(nu), vp(ws), wb,
+              stream_ptr())
+    torch.cuda.synchronize()
+    u = nu.value
+    uq, ct, inv, off = [o.cpu().numpy() for o in outs]
+    return u, uq[:u], ct[:u], inv[:n], off[:u]
+
+
+def check_against_oracle(keys):
+    u, uq, ct, inv, off = gpu_dedup(keys)
+    ru, rc, rinv, roff = O.dedup(keys)
+    assert u == ru.size
+    assert np.array_equal(uq, ru) and np.array_equal(ct, rc)
+    assert np.array_equal(inv, rinv) and np.array_equal(off, roff)
+    # invariants: ascending unique keys, counts sum, inverse covers every position once
+    assert np.all(np.diff(uq) > 0)
+    assert ct.sum() == keys.size
+    assert np.array_equal(np.sort(inv), np.arange(keys.size))
+    for k in range(min(u, 50)):
+        pos = inv[off[k]:off[k] + ct[k]]
+        assert np.all(keys[pos] == uq[k]) and np.all(np.diff(pos) > 0)
+
+
+@pytest.mark.parametrize("dtype", [np.int64, np.int32])
+def test_dedup_edge_cases(dtype):
+    check_against_oracle(np.arange(1000, dtype=dtype)[::-1].copy())           # all unique
+    check_against_oracle(np.full(3000, 42, dtype=dtype))                      # all identical
+    check_against_oracle(np.array([5], dtype=dtype))                          # single key
+    check_against_oracle(np.array([3, -1, 7, -1, -(2**31 - 1), 3, 0], dtype=dtype))  # signed order
+    u, *_ = gpu_dedup(np.zeros(0, dtype=dtype))                                # empty
+    assert u == 0
+
+
+@pytest.mark.parametrize("n,hi", [(5000, 100), (70000, 2**40), (262144, 50_000_000)])
+def test_dedup_random(n, hi):
+    rng = np.random.default_rng(n)
+    keys = rng.integers(-hi, hi, size=n).astype(np.int64)
+    check_against_oracle(keys)
+
+
+def test_dedup_benchmark_zipf_keys_and_gather():
+    """C2 shape: 262,144 Zipf(1.05) keys over 50M rows (reference generator),
+    on a smaller table of the same row width (keys reduced modulo its rows)."""
+    rng = np.random.default_rng(3)
+    n, rows, dim = 262144, 200000, 128
+    x = rng.random(n)
+    keys = O.power_law(x, 1, 50_000_000, 1.05) % rows
+    check_against_oracle(keys)
+    tb = float_table(rng, rows, dim, O.F16, dyadic_values=False)
+    d_tab, d_keys = to_dev(tb.reshape(-1)), to_dev(keys)
+    out = torch.zeros((n, dim * 2), dtype=torch.uint8, device="cuda")
+    ws, wb = workspace(n)
+    _lib.call("nve_amd_dedup_gather", _lib.KEY_INT64, n, vp(d_keys), vp(d_tab), rows, dim * 2, vp(out),
+              dim * 2, vp(ws), wb, stream_ptr())
+    torch.cuda.synchronize()
+    ref, hits = O.gather(keys, np.ascontiguousarray(tb).reshape(-1), dim * 2, rows)
+    assert hits == n
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def test_dedup_gather_int32_and_out_of_range_keys_untouched():
+    rng = np.random.default_rng(5)
+    rows, dim = 3000, 24
+    tb = float_table(rng, rows, dim, O.F32)
+    keys = rng.integers(-50, rows + 50, size=5000).astype(np.int32)
+    d_tab, d_keys = to_dev(tb.reshape(-1)), to_dev(keys)
+    out = torch.full((keys.size, dim * 4), 0xCD, dtype=torch.uint8, device="cuda")
+    ws, wb = workspace(keys.size)
+    _lib.call("nve_amd_dedup_gather", _lib.KEY_INT32, keys.size, vp(d_keys), vp(d_tab), rows, dim * 4,
+              vp(out), dim * 4, vp(ws), wb, stream_ptr())
+    torch.cuda.synchronize()
+    exp = np.full((keys.size, dim * 4), 0xCD, np.uint8)
+    ref, _ = O.gather(keys, np.ascontiguousarray(tb).reshape(-1), dim * 4, rows, out=exp)
+    assert np.array_equal(out.cpu().numpy(), ref)
