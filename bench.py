@@ -19,6 +19,7 @@ Reported beside the throughput:
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -127,8 +128,189 @@ def read_ceiling(torch, lib, stream, counts):
     return res
 
 
+def time_steps(torch, stream, step, warmup, steps):
+    """Mean milliseconds per step between HIP events recorded on `stream`."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def fill_rows(torch, rows, width, make_chunk, seed):
+    """Device table of rows x width bytes filled chunk by chunk."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    t = torch.empty((rows, width), dtype=torch.uint8, device="cuda")
+    chunk = 1 << 22
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        t[r0:r1] = make_chunk(r1 - r0, gen)
+    return t
+
+
+def quant_rows_xi8a(torch, n, gen):
+    """int8 U[-127, 127], fp32 scale log-U[1e-3, 1e-1], fp32 offset N(0, 0.01)."""
+    q = torch.randint(-127, 128, (n, 256), device="cuda", dtype=torch.int16, generator=gen).to(torch.int8)
+    u = torch.rand(n, device="cuda", generator=gen)
+    scale = torch.exp(math.log(1e-3) + u * (math.log(1e-1) - math.log(1e-3)))
+    off = torch.randn(n, device="cuda", generator=gen) * 0.01
+    return torch.cat([q.view(torch.uint8), scale.view(n, 1).view(torch.uint8), off.view(n, 1).view(torch.uint8)], 1)
+
+
+def quant_rows_e4m3(torch, n, gen):
+    """OCP e4m3 codes (NaN codes remapped to 448) and an fp32 scale log-U[1e-3, 1e-1]."""
+    q = torch.randint(0, 256, (n, 256), device="cuda", dtype=torch.int16, generator=gen).to(torch.uint8)
+    q[(q & 0x7F) == 0x7F] -= 1
+    u = torch.rand(n, device="cuda", generator=gen)
+    scale = torch.exp(math.log(1e-3) + u * (math.log(1e-1) - math.log(1e-3)))
+    return torch.cat([q, scale.view(n, 1).view(torch.uint8)], 1)
+
+
+def run_workload(args, torch, _lib):
+    """Parity-test configurations of BASELINE.json measured the same way
+    (not the contract line): c2 (dedup then gather), c4a / c4b (dequant),
+    c5 (26-table jagged weighted mean)."""
+    L = _lib.load()
+    stream = torch.cuda.Stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    w = args.workload
+    kgen = torch.Generator(device="cuda")
+    kgen.manual_seed(1)
+    cfg_out = {"workload": w}
+    if w in ("c2", "c4a", "c4b"):
+        if w == "c2":
+            rows, width, nkeys, alpha = 50_000_000, 256, 262144, 1.05
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(0)
+            table = torch.empty((rows, 128), dtype=torch.float16, device="cuda")
+            for r0 in range(0, rows, 1 << 24):
+                table[r0:min(rows, r0 + (1 << 24))].normal_(0.0, 0.02, generator=gen)
+            vdt, out_w, odt = _lib.DT_F16, 256, _lib.DT_F16
+        elif w == "c4a":
+            rows, width, nkeys, alpha = 100_000_000, 264, 131072, 1.05
+            table = fill_rows(torch, rows, width, lambda n, g: quant_rows_xi8a(torch, n, g), 0)
+            vdt, out_w, odt = _lib.DT_XI8A_F32, 512, _lib.DT_F16
+        else:
+            rows, width, nkeys, alpha = 100_000_000, 260, 131072, 1.05
+            table = fill_rows(torch, rows, width, lambda n, g: quant_rows_e4m3(torch, n, g), 0)
+            vdt, out_w, odt = _lib.DT_XE4M3_F32, 1024, _lib.DT_F32
+        pg = torch.Generator(device="cuda")
+        pg.manual_seed(31337)
+        perm = torch.randperm(rows, generator=pg, device="cuda", dtype=torch.int64)
+        batches = [power_law_keys(torch, nkeys, rows, alpha, kgen, perm) for _ in range(args.batches)]
+        del perm
+        out = torch.empty((nkeys, out_w), dtype=torch.uint8, device="cuda")
+        lc = L.nve_gpu_embedding_layer_config_default()
+        lc.layer_name = b"bench"
+        lc.embedding_table = table.data_ptr()
+        lc.num_embeddings = rows
+        lc.embedding_width_in_bytes = width
+        lc.value_dtype = vdt
+        layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("nve_gpu_embedding_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), None)
+        _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
+        kp = [ctypes.c_void_p(b.data_ptr()) for b in batches]
+        op = ctypes.c_void_p(out.data_ptr())
+        if w == "c2":
+            wsb = ctypes.c_uint64()
+            _lib.call("nve_amd_dedup_workspace_size", nkeys, ctypes.byref(wsb))
+            ws = torch.empty(int(wsb.value), dtype=torch.uint8, device="cuda")
+
+            def step(i):
+                _lib.call("nve_amd_dedup_gather", _lib.KEY_INT64, nkeys, kp[i % len(kp)],
+                          ctypes.c_void_p(table.data_ptr()), rows, width, op, width,
+                          ctypes.c_void_p(ws.data_ptr()), wsb.value, sp)
+
+            def plain(i):
+                _lib.check(L.nve_layer_lookup(layer, ctx, nkeys, kp[i % len(kp)], op, width, None, None))
+
+            ms_plain = time_steps(torch, stream, plain, args.warmup, args.steps)
+            cfg_out["plain_gather_ms"] = round(ms_plain, 6)
+            alg = nkeys * 8 + nkeys * width + nkeys * width
+        else:
+            def step(i):
+                _lib.check(L.nve_layer_lookup_pooled(layer, ctx, nkeys, kp[i % len(kp)], op, out_w, None,
+                                                     _lib.POOL_CONCAT, 0, None, 0, 0, None, 0, odt, None))
+
+            alg = nkeys * 8 + nkeys * width + nkeys * out_w
+        ms = time_steps(torch, stream, step, args.warmup, args.steps)
+        cfg_out.update({"table_rows": rows, "row_bytes": width, "keys_per_batch": nkeys, "zipf_alpha": alpha})
+        _lib.call("nve_context_wait", ctx)
+        _lib.call("nve_context_destroy", ctx)
+        _lib.call("nve_layer_destroy", layer)
+        kernel = "sort + gather_kernel" if w == "c2" else "gather_kernel (dequant)"
+    elif w == "c5":
+        T, B, dim = 26, 8192, 128
+        cg = torch.Generator()
+        cg.manual_seed(4)
+        cards = torch.exp(torch.log(torch.tensor(1e3)) + torch.rand(T, generator=cg, dtype=torch.float64)
+                          * (torch.log(torch.tensor(4e7)) - torch.log(torch.tensor(1e3)))).long().tolist()
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0)
+        tables = []
+        for c in cards:
+            t = torch.empty((c, dim), dtype=torch.float16, device="cuda")
+            for r0 in range(0, c, 1 << 24):
+                t[r0:min(c, r0 + (1 << 24))].normal_(0.0, 0.02, generator=gen)
+            tables.append(t)
+        lg = torch.Generator(device="cuda")
+        lg.manual_seed(3)
+        wg = torch.Generator(device="cuda")
+        wg.manual_seed(2)
+        sets = []
+        for _ in range(max(2, args.batches // 4)):
+            lens = torch.poisson(torch.full((T, B), 20.0, device="cuda"), generator=lg).clamp_(1, 100).long()
+            off = torch.zeros(T * B + 1, dtype=torch.int64, device="cuda")
+            off[1:] = torch.cumsum(lens.view(-1), 0)
+            ks = []
+            for t in range(T):
+                pg = torch.Generator(device="cuda")
+                pg.manual_seed(31337 + t)
+                perm = torch.randperm(cards[t], generator=pg, device="cuda", dtype=torch.int64)
+                ks.append(power_law_keys(torch, int(lens[t].sum().item()), cards[t], 1.1, kgen, perm))
+            keys = torch.cat(ks)
+            wts = torch.rand(keys.numel(), device="cuda", generator=wg)
+            sets.append((keys, off, wts))
+        nkeys = sum(s[0].numel() for s in sets) // len(sets)
+        out = torch.empty((B, T, dim), dtype=torch.float32, device="cuda")
+        ptrs = (ctypes.c_void_p * T)(*[t.data_ptr() for t in tables])
+
+        def step(i):
+            keys, off, wts = sets[i % len(sets)]
+            _lib.call("nve_amd_find_and_pool_multi", _lib.KEY_INT64, T, ptrs, dim * 2, _lib.DT_F16, B,
+                      keys.numel(), ctypes.c_void_p(keys.data_ptr()), ctypes.c_void_p(off.data_ptr()),
+                      ctypes.c_void_p(wts.data_ptr()), _lib.DT_F32, _lib.POOL_WMEAN, _lib.DT_F32,
+                      ctypes.c_void_p(out.data_ptr()), sp)
+
+        ms = time_steps(torch, stream, step, args.warmup, args.steps)
+        alg = nkeys * (8 + 4 + dim * 2) + (T * B + 1) * 8 + B * T * dim * 4
+        cfg_out.update({"tables": T, "cardinalities": cards, "total_rows": sum(cards), "batch": B,
+                        "mean_keys_per_batch": nkeys, "pooling": "weighted_mean", "output_dtype": "f32"})
+        kernel = "pool_kernel (multi-table)"
+    else:
+        raise SystemExit(f"unknown workload {w}")
+    achieved = alg / (ms * 1e-3) / 1e9
+    res = {"metric": METRIC, "value": round(nkeys / (ms * 1e-3), 1), "unit": "lookups/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic", "config": cfg_out,
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "kernel": kernel, "alg_bytes_per_launch": alg}}
+    log(f"{w}: {ms * 1000:.2f} us/step, {res['value'] / 1e9:.2f} G lookups/s, {achieved:.0f} GB/s")
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="c2pool", choices=["c2pool", "c2", "c4a", "c4b", "c5"],
+                    help="c2pool (default, the metric's configuration) or a parity configuration")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -166,6 +348,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}), flush=True)
         return
+    if args.workload != "c2pool":
+        return run_workload(args, torch, _lib)
     rows, dim, bags, hot = args.rows, args.dim, args.bags, args.hotness
     nkeys = bags * hot
     width = dim * 2

@@ -4,6 +4,7 @@
 // handles are rejected with NVE_ERROR_INVALID_ARGUMENT before any work; every
 // exception becomes a status (nve_c_api_internal.hpp:48-92) with its message
 // kept in thread-local storage for nve_get_last_error.
+#include <algorithm>
 #include <cstring>
 #include <new>
 
@@ -715,6 +716,70 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
                 "unroll_hint must be 0, 8 or 16");
   p.force_unroll = unroll_hint;
   NVE_HIP(launch_pool(p, (hipStream_t)stream));
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_find_and_pool_multi(nve_key_type_t key_type, int64_t num_tables,
+                                         const void* const* tables, int64_t row_size_in_bytes,
+                                         nve_data_type_t value_dtype, int64_t batch_size,
+                                         int64_t num_keys, const void* keys, const void* offsets,
+                                         const void* weights, nve_data_type_t weight_type,
+                                         nve_pooling_type_t pooling_type,
+                                         nve_data_type_t output_type, void* output, void* stream) {
+  C_TRY
+  const int kb = key_bytes_of(key_type);
+  const int vdt = dtype_in(value_dtype);
+  const int odt = dtype_in(output_type);
+  NVE_CHECK_ARG(num_tables > 0 && tables != nullptr, "tables must not be empty");
+  NVE_CHECK_ARG(batch_size > 0 && num_keys >= 0, "Invalid batch_size / num_keys");
+  NVE_CHECK_ARG(offsets != nullptr && output != nullptr && (keys != nullptr || num_keys == 0),
+                "keys, offsets and output must not be NULL");
+  NVE_CHECK_ARG(vdt == kF32 || vdt == kF16 || is_rowwise(vdt), "Unsupported value type ", vdt);
+  NVE_CHECK_ARG(odt == kF32 || odt == kF16, "Output type must be Float32 or Float16");
+  NVE_CHECK_ARG(pooling_type >= NVE_POOL_SUM && pooling_type <= NVE_POOL_WEIGHTED_MEAN,
+                "Multi-table pooling needs a reducing pooling type");
+  const bool weighted = is_weighted_pooling(pooling_type);
+  if (weighted) {
+    NVE_CHECK_ARG(weights != nullptr, "Sparse weights are required for weighted pooling");
+    NVE_CHECK_ARG(dtype_in(weight_type) == kF32 || dtype_in(weight_type) == kF16,
+                  "Unsupported weight type");
+  }
+  const int64_t meta = meta_bytes(vdt);
+  NVE_CHECK_ARG(row_size_in_bytes > meta, "Invalid row size");
+  if (is_rowwise(vdt)) NVE_CHECK_ARG(row_size_in_bytes % 2 == 0, "Quantized rows must have an even width");
+  const int64_t count = (row_size_in_bytes - meta) / value_elem_bytes(vdt);
+  const int64_t oes = dtype_size(odt);
+  for (int64_t t = 0; t < num_tables; ++t) NVE_CHECK_ARG(tables[t] != nullptr, "table ", t, " is NULL");
+  for (int64_t t0 = 0; t0 < num_tables; t0 += kMaxPoolTables) {
+    const int64_t nt = std::min<int64_t>(kMaxPoolTables, num_tables - t0);
+    PoolLaunch p{};
+    p.keys = keys;
+    p.key_bytes = kb;
+    p.num_keys = num_keys;
+    p.offsets = static_cast<const uint8_t*>(offsets) + (size_t)t0 * batch_size * kb;
+    p.num_bags = nt * batch_size;
+    p.weighted = weighted;
+    p.mean = is_mean_pooling(pooling_type);
+    if (weighted) {
+      p.weights = weights;
+      p.weight_dtype = dtype_in(weight_type);
+    }
+    p.src.row_bytes = (uint64_t)row_size_in_bytes;
+    p.src.load_indices = 1;
+    p.src.table = static_cast<const uint8_t*>(tables[t0]);
+    p.stored_dtype = vdt;
+    p.count = count;
+    p.out = static_cast<uint8_t*>(output) + t0 * count * oes;
+    p.out_stride = num_tables * count * oes;
+    p.out_dtype = odt;
+    p.num_tables = (int)nt;
+    p.keys_per_bag = std::max<int64_t>(1, num_keys / (num_tables * batch_size));
+    p.bags_per_table = batch_size;
+    p.out_table_stride = count * oes;
+    for (int64_t t = 0; t < nt; ++t) p.tables[t] = static_cast<const uint8_t*>(tables[t0 + t]);
+    NVE_HIP(launch_pool(p, (hipStream_t)stream));
+  }
   return NVE_SUCCESS;
   C_CATCH
 }

@@ -11,6 +11,8 @@
 
 namespace nve_amd {
 
+constexpr int kMaxPoolTables = 64;  // tables one multi-table pooling launch can address
+
 // Where rows come from (see resolve_row in device_common.cuh).
 struct RowSource {
   const uint8_t* table;      // linear table / backing table (may be null with a cache)
@@ -64,6 +66,14 @@ struct PoolLaunch {
   unsigned long long* miss_counter;
   int force_split;   // 0: heuristic; > 0: groups per bag (power of two); < 0: one group per bag
   int force_unroll;  // 0: heuristic; 8 or 16: row loads in flight per lane group
+  // Several tables in one launch (num_tables > 0): bag g belongs to table
+  // g / bags_per_table, reads rows of tables[table] (linear, no cache) and writes
+  // output row (g % bags_per_table) * out_stride + table * out_table_stride.
+  int num_tables;
+  int64_t keys_per_bag;  // mean bag length for the geometry choice (0: num_keys / num_bags)
+  int64_t bags_per_table;
+  int64_t out_table_stride;
+  const uint8_t* tables[kMaxPoolTables];
 };
 
 hipError_t launch_gather(const GatherLaunch& a, hipStream_t stream);

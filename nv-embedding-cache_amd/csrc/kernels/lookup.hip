@@ -120,6 +120,14 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
 // ---------------------------------------------------------------------------
 // find-and-pool: one output row per bag
 // ---------------------------------------------------------------------------
+// Output row of bag g (one table, or bag g of several tables in one launch).
+__device__ __forceinline__ uint8_t* bag_out_row(const PoolLaunch& a, int64_t g) {
+  uint8_t* out = reinterpret_cast<uint8_t*>(a.out);
+  if (a.num_tables > 0)
+    return out + (g % a.bags_per_table) * a.out_stride + (g / a.bags_per_table) * a.out_table_stride;
+  return out + g * a.out_stride;
+}
+
 template <int SDT, int VB, int U>
 __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, int gpb_shift,
                                                    int passes) {
@@ -151,6 +159,9 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
       e = s + a.hotness;
     }
   }
+  // the bag's table (several tables in one launch) and output row
+  RowSource src = a.src;
+  if (a.num_tables > 0 && live) src.table = a.tables[bag / a.bags_per_table];
   int64_t cs = s, ce = e;
   if (gpb > 1 && e > s) {
     const int64_t per = (e - s + gpb - 1) >> gpb_shift;
@@ -181,7 +192,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
       if (kk < ce) {
         const int64_t key = a.src.load_indices ? load_key(a.keys, a.key_bytes, kk) : kk;
         bool miss;
-        addr = resolve_row(a.src, a.key_bytes, key, kk, &miss);
+        addr = resolve_row(src, a.key_bytes, key, kk, &miss);
         if (p == 0 && miss) misses++;
         if (weighted) w = load_weight(a.weights, a.weight_dtype, kk);
       }
@@ -227,8 +238,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
 #pragma unroll
           for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
         }
-        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride +
-                     ((int64_t)p * G + gl) * E * out_es;
+        uint8_t* o = bag_out_row(a, bag) + ((int64_t)p * G + gl) * E * out_es;
         store_out<E>(o, acc, out_f16);
       }
       continue;
@@ -251,8 +261,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
 #pragma unroll
           for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
         }
-        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride +
-                     ((int64_t)p * G + gl) * E * out_es;
+        uint8_t* o = bag_out_row(a, bag) + ((int64_t)p * G + gl) * E * out_es;
         store_out<E>(o, acc, out_f16);
       }
       continue;
@@ -304,8 +313,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
           }
           v = (d == 0.0f) ? 0.0f : v / d;
         }
-        uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bg * a.out_stride +
-                     ((int64_t)p * row_elems + x) * out_es;
+        uint8_t* o = bag_out_row(a, bg) + ((int64_t)p * row_elems + x) * out_es;
         if (out_f16)
           *reinterpret_cast<uint16_t*>(o) = f2h(v);
         else
@@ -481,13 +489,23 @@ bool pool_geometry(const PoolLaunch& a, PoolGeometry* g) {
   const int esize = value_elem_bytes(a.stored_dtype);
   const int64_t area = a.count * esize;
   const int out_es = a.out_dtype == kF16 ? 2 : 4;
-  const int vb = pick_vb(max_vb_of(a.stored_dtype), esize, out_es, area, a.src, a.out, a.out_stride);
+  int vb = pick_vb(max_vb_of(a.stored_dtype), esize, out_es, area, a.src, a.out, a.out_stride);
+  // several tables: every table and every table's output column must allow it
+  for (int t = 0; t < a.num_tables && vb > 0; ++t) {
+    RowSource st = a.src;
+    st.table = a.tables[t];
+    vb = pick_vb(vb, esize, out_es, area, st, a.out, a.out_stride);
+  }
+  if (a.num_tables > 0) {
+    while (vb >= esize && a.out_table_stride % ((vb / esize) * out_es) != 0) vb >>= 1;
+    if (vb < esize) vb = 0;
+  }
   if (vb == 0) return false;
   const int64_t nv = area / vb;
   const int G = nv >= 64 ? 64 : pow2_ceil(nv);
   const int passes = (int)((nv + G - 1) / G);
   const int64_t bags = a.num_bags;
-  const int64_t avg = bags > 0 ? a.num_keys / bags : 0;
+  const int64_t avg = a.keys_per_bag > 0 ? a.keys_per_bag : (bags > 0 ? a.num_keys / bags : 0);
   int gpb = 1;
   if (a.force_split > 0) {
     gpb = pow2_ceil(a.force_split);
