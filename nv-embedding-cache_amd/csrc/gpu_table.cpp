@@ -84,7 +84,8 @@ void GpuTable::find(ExecutionContext& ctx, int64_t n, const void* keys, uint64_t
   NVE_CHECK(value_sizes == nullptr, "value_sizes must be nullptr for GPU table");
   if (n <= 0) return;
   NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
-  const hipStream_t stream = ctx.lookup_stream();
+  StreamQueue q(ctx.lookup_stream(), cfg_.private_stream);
+  const hipStream_t stream = q.stream;
   const void* d_keys = device_input(ctx, "keys", keys, (size_t)n * key_bytes_, stream);
   const bool uvm = cfg_.uvm_table != nullptr;
   uint64_t* d_mask = nullptr;
@@ -132,7 +133,8 @@ void GpuTable::find(ExecutionContext& ctx, int64_t n, const void* keys, uint64_t
 void GpuTable::find_and_pool(ExecutionContext& ctx, int64_t n, const void* d_keys,
                              const PoolingParams& pp, void* d_output, int64_t output_stride) {
   ScopedDevice sd(cfg_.device_id);
-  const hipStream_t stream = ctx.lookup_stream();
+  StreamQueue q(ctx.lookup_stream(), cfg_.private_stream);
+  const hipStream_t stream = q.stream;
   const int vdt = cfg_.value_dtype;
   const int64_t count =
       is_rowwise(vdt) ? (cfg_.row_size_in_bytes - meta_bytes(vdt)) / value_elem_bytes(vdt)
@@ -187,7 +189,8 @@ void GpuTable::erase(ExecutionContext& ctx, int64_t n, const void* keys) {
   NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
   std::lock_guard<std::mutex> mk(modify_mu_);
   std::unique_lock<std::shared_mutex> lk(uvm_mu_);
-  const hipStream_t stream = ctx.modify_stream();
+  StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
+  const hipStream_t stream = q.stream;
   const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, stream);
   NVE_HIP(launch_cache_erase(tags_, d_keys, n, key_bytes_, num_sets_, cfg_.invalid_key, stream));
   NVE_HIP(hipStreamSynchronize(stream));
@@ -197,7 +200,8 @@ void GpuTable::clear(ExecutionContext& ctx) {
   ScopedDevice sd(cfg_.device_id);
   std::lock_guard<std::mutex> mk(modify_mu_);
   std::unique_lock<std::shared_mutex> lk(uvm_mu_);
-  const hipStream_t stream = ctx.modify_stream();
+  StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
+  const hipStream_t stream = q.stream;
   const int64_t ways = (int64_t)num_sets_ * kWays;
   NVE_HIP(launch_fill_tags(tags_, ways, key_bytes_, cfg_.invalid_key, stream));
   NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), ways, 0, stream));

@@ -158,8 +158,9 @@ class GpuTable {
   std::shared_mutex& uvm_mutex() { return uvm_mu_; }
 
  private:
-  void modify_insert(ExecutionContext& ctx, int64_t n, const void* keys, const uint8_t* rows,
-                     int64_t row_stride, bool from_uvm);
+  // runs on stream s (the modify stream or the table's private stream)
+  void modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
+                     const uint8_t* rows, int64_t row_stride, bool from_uvm);
   void build_decay_table();
   int key_bytes_;
   GPUTableConfig cfg_;

@@ -77,10 +77,10 @@ void GpuTable::insert(ExecutionContext& ctx, int64_t n, const void* keys, int64_
   NVE_CHECK(values != nullptr, "Invalid cache insert params");
   NVE_CHECK(value_size == cfg_.row_size_in_bytes, "Unsupported value_size");
   NVE_CHECK_ARG(value_stride >= value_size, "value_stride is smaller than value_size");
-  const hipStream_t stream = ctx.modify_stream();
+  StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
   const void* d_vals = device_input(ctx, "insert_values", values,
-                                    (size_t)(n - 1) * value_stride + value_size, stream);
-  modify_insert(ctx, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
+                                    (size_t)(n - 1) * value_stride + value_size, q.stream);
+  modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
 }
 
 void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* keys) {
@@ -88,15 +88,15 @@ void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* key
   NVE_CHECK(cfg_.uvm_table != nullptr, "insert_from_uvm requires a UVM table");
   if (n <= 0) return;
   NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
-  modify_insert(ctx, n, keys, static_cast<const uint8_t*>(cfg_.uvm_table), cfg_.row_size_in_bytes,
-                true);
+  StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
+  modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(cfg_.uvm_table),
+                cfg_.row_size_in_bytes, true);
 }
 
-void GpuTable::modify_insert(ExecutionContext& ctx, int64_t n, const void* keys,
+void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
                              const uint8_t* rows, int64_t row_stride, bool from_uvm) {
   NVE_CHECK(n <= (int64_t)UINT32_MAX, "Too many keys for one insert");
   std::lock_guard<std::mutex> mk(modify_mu_);
-  const hipStream_t s = ctx.modify_stream();
   const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, s);
 
   // ---- scratch (grow-only, per context) ----

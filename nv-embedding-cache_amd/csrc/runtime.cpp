@@ -23,6 +23,37 @@ ScopedDevice::~ScopedDevice() {
 }
 
 // ---------------------------------------------------------------------------
+namespace {
+hipEvent_t order_event() {
+  thread_local std::map<int, hipEvent_t> events;
+  int dev = 0;
+  NVE_HIP(hipGetDevice(&dev));
+  hipEvent_t& e = events[dev];
+  if (!e) NVE_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  return e;
+}
+}  // namespace
+
+StreamQueue::StreamQueue(hipStream_t caller, hipStream_t run)
+    : stream(run ? run : caller), caller_(caller) {
+  if (stream != caller_) {
+    hipEvent_t e = order_event();
+    NVE_HIP(hipEventRecord(e, caller_));
+    NVE_HIP(hipStreamWaitEvent(stream, e, 0));
+  }
+}
+
+StreamQueue::~StreamQueue() {
+  if (stream != caller_) {
+    try {
+      hipEvent_t e = order_event();  // created by the constructor on this thread and device
+      if (hipEventRecord(e, stream) == hipSuccess) (void)hipStreamWaitEvent(caller_, e, 0);
+    } catch (...) {
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 ThreadPool::ThreadPool(int64_t num_workers) {
   if (num_workers <= 0) {
     const int64_t cores = (int64_t)std::thread::hardware_concurrency();

@@ -76,6 +76,23 @@ class ScopedDevice {
   int prev_ = -1;
 };
 
+// Runs a table operation on `run` (a table's private stream) when it is set,
+// else on `caller`: work queued on `caller` before the scope happens-before
+// the operation, and work queued on `caller` after the scope waits for it
+// (StreamCoordinator, layer_utils.hpp:88-118).  The ordering uses one reusable
+// event per thread and device: a stream wait binds to the record made before it.
+class StreamQueue {
+ public:
+  StreamQueue(hipStream_t caller, hipStream_t run);
+  ~StreamQueue();
+  StreamQueue(const StreamQueue&) = delete;
+  StreamQueue& operator=(const StreamQueue&) = delete;
+  const hipStream_t stream;
+
+ private:
+  const hipStream_t caller_;
+};
+
 // ---------------------------------------------------------------------------
 // thread pool (SimpleThreadPool: default workers = max(cores - 2, 1))
 // ---------------------------------------------------------------------------

@@ -1,0 +1,494 @@
+"""pynve.nve: layer bindings over the C ABI of libnve_amd.so.
+
+Mirrors the reference's pybind11 module `pynve.nve`
+(python/pynve/bindings/python_binding.cu:149-392, binding_layers.hpp:50-788):
+the same class names, constructor arguments, method names and argument
+meaning.  Keys are int64; every pointer argument is a raw address (an int),
+streams are `hipStream_t` values (`torch.cuda.current_stream().cuda_stream`
+on ROCm).  Lookups take one execution context per stream, created on first
+use, as `NVEmbedBinding::get_exec_context` does (binding_layers.hpp:352-366).
+
+Memory blocks: device memory comes from torch's allocator, host memory from
+`hipHostMalloc` (pinned and mapped into the GPU's address space).  A
+`ManagedMemBlock` (reference: cudaMallocManaged + preferred location host +
+accessed-by the GPUs, memblock.cpp:111-134) is pinned host memory here: with
+XNACK off, that is the memory the MI355X reads over the host link without
+page faults, which is what the reference's advice arranges.
+
+Out of this build (raise NotImplementedInBuild): the training calls
+(`concat_backprop`, `pooling_backprop`), `update` / `accumulate` on GPU tables,
+HostEmbedding / HierarchicalEmbedding layers, the parameter-server tables and
+the multi-process memory blocks (NVL / MPI / Dist*).
+"""
+import ctypes
+import json
+import logging
+import threading
+from enum import IntEnum
+
+from . import _lib
+
+_log = logging.getLogger("pynve")
+
+
+class DataType_t(IntEnum):
+    """nve::DataType_t (nve_types.hpp:59-72), the ids the C ABI uses."""
+    Unknown = 0
+    Float32 = 1
+    BFloat = 2
+    Float16 = 3
+    E4M3 = 4
+    E5M2 = 5
+    Float64 = 6
+
+
+class PoolingType_t(IntEnum):
+    """nve::PoolingType_t (python_binding.cu:204-210)."""
+    Concatenate = 0
+    Sum = 1
+    Mean = 2
+    WeightedSum = 3
+    WeightedMean = 4
+
+
+class MemBlockType(IntEnum):
+    """nve::MemBlockType (memblock.hpp:29-36)."""
+    Linear = 0
+    NVL = 1
+    MPI = 2
+    Managed = 3
+    User = 4
+    Host = 5
+
+
+_DTYPE_SIZE = {DataType_t.Float32: 4, DataType_t.BFloat: 2, DataType_t.Float16: 2,
+               DataType_t.E4M3: 1, DataType_t.E5M2: 1, DataType_t.Float64: 8}
+
+
+def dtype_size(dtype):
+    """Bytes per element (nve_types.hpp dtype_size)."""
+    try:
+        return _DTYPE_SIZE[DataType_t(dtype)]
+    except (KeyError, ValueError):
+        raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, f"dtype {dtype!r} has no element size")
+
+
+class EmbedLayerConfig:
+    """Per-layer options (binding_layers.hpp:50-65); same fields and defaults."""
+
+    _FIELDS = ("logging_interval", "kernel_mode", "kernel_mode_value_1", "kernel_mode_value_2",
+               "max_modify_size", "default_row_index", "default_embedding")
+
+    def __init__(self):
+        self.logging_interval = -1
+        self.kernel_mode = 0
+        self.kernel_mode_value_1 = 0
+        self.kernel_mode_value_2 = 0
+        self.max_modify_size = 0
+        self.default_row_index = -1
+        self.default_embedding = []
+
+    def to_json(self):
+        return json.dumps({f: getattr(self, f) for f in self._FIELDS})
+
+
+# ---------------------------------------------------------------------------
+# memory blocks (memblock.hpp / memblock.cpp)
+# ---------------------------------------------------------------------------
+
+_hip = None
+
+
+def _hip_lib():
+    global _hip
+    if _hip is None:
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipHostMalloc.restype = ctypes.c_int
+        h.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+        h.hipHostFree.restype = ctypes.c_int
+        h.hipHostFree.argtypes = [ctypes.c_void_p]
+        h.hipMemcpy.restype = ctypes.c_int
+        h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _hip = h
+    return _hip
+
+
+class MemBlock:
+    """A block of memory a layer reads its rows from; the layer keeps a
+    reference so the block outlives it (binding_layers.hpp:529-788)."""
+
+    def __init__(self, kind, ptr, size):
+        self._type = MemBlockType(kind)
+        self._ptr = int(ptr)
+        self._size = int(size)
+
+    def get_ptr(self):
+        return self._ptr
+
+    def get_handle(self):
+        return self._ptr
+
+    def get_type(self):
+        return self._type
+
+    def get_size_in_bytes(self):
+        return self._size
+
+    def copy_from(self, src):
+        """Copy a C-contiguous buffer (numpy array, bytes, ...) into the block,
+        bounds-checked (python_binding.cu:235-261)."""
+        mv = memoryview(src)
+        if not mv.c_contiguous:
+            raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT,
+                                       "copy_from: source buffer must be C-contiguous")
+        nbytes = mv.nbytes
+        if nbytes > self._size:
+            raise IndexError(f"copy_from: source is {nbytes} bytes but memblock holds "
+                             f"{self._size} bytes")
+        if nbytes == 0:
+            return
+        import numpy as np
+        src_bytes = np.frombuffer(mv.cast("B"), dtype=np.uint8)
+        rc = _hip_lib().hipMemcpy(self._ptr, src_bytes.ctypes.data, nbytes, 4)  # hipMemcpyDefault
+        if rc != 0:
+            raise _lib.NVEError(_lib.HIP_ERROR, f"copy_from: hipMemcpy failed ({rc})")
+
+
+class UserMemBlock(MemBlock):
+    """Caller-owned memory (memblock.hpp UserMemBlock): nothing is freed."""
+
+    def __init__(self, ptr, size):
+        super().__init__(MemBlockType.User, ptr, size)
+
+
+class _PinnedHost(MemBlock):
+    def __init__(self, kind, size):
+        p = ctypes.c_void_p()
+        if size > 0:
+            rc = _hip_lib().hipHostMalloc(ctypes.byref(p), size, 0)
+            if rc != 0 or not p.value:
+                raise _lib.NVEError(_lib.OUT_OF_MEMORY,
+                                    f"hipHostMalloc of {size} bytes failed ({rc})")
+        super().__init__(kind, p.value or 0, size)
+
+    def __del__(self):
+        if getattr(self, "_ptr", 0) and _hip is not None:
+            _hip.hipHostFree(self._ptr)
+            self._ptr = 0
+
+
+class HostMemBlock(_PinnedHost):
+    """Pinned host memory (memblock.cpp:93-105)."""
+
+    def __init__(self, row_size, num_embeddings, dtype):
+        super().__init__(MemBlockType.Host, int(row_size) * int(num_embeddings) * dtype_size(dtype))
+
+
+class ManagedMemBlock(_PinnedHost):
+    """Host-resident memory the GPUs read directly (memblock.cpp:111-134);
+    pinned and GPU-mapped on this build (see the module docstring)."""
+
+    def __init__(self, row_size, num_embeddings, dtype, gpu_ids=()):
+        self.gpu_ids = list(gpu_ids)
+        super().__init__(MemBlockType.Managed, int(row_size) * int(num_embeddings) * dtype_size(dtype))
+
+
+class LinearMemBlock(MemBlock):
+    """Device memory of `device_id`, or pinned host memory when it is negative
+    (memblock.cpp:27-50)."""
+
+    def __init__(self, row_size, num_embeddings, dtype, device_id=-1):
+        size = int(row_size) * int(num_embeddings) * dtype_size(dtype)
+        self.device_id = int(device_id)
+        if self.device_id < 0:
+            self._host = _PinnedHost(MemBlockType.Linear, size)
+            super().__init__(MemBlockType.Linear, self._host.get_ptr(), size)
+        else:
+            import torch
+            self._tensor = torch.empty(size, dtype=torch.uint8, device=f"cuda:{self.device_id}")
+            super().__init__(MemBlockType.Linear, self._tensor.data_ptr(), size)
+
+
+def _not_in_build(what):
+    raise _lib.NotImplementedInBuild(_lib.NOT_IMPLEMENTED, f"{what} is not part of this build")
+
+
+class NVLMemBlock(MemBlock):
+    def __init__(self, *args, **kwargs):
+        _not_in_build("NVLMemBlock (multi-GPU shared tables)")
+
+
+class MPIMemBlock(MemBlock):
+    def __init__(self, *args, **kwargs):
+        _not_in_build("MPIMemBlock (multi-process shared tables)")
+
+
+class Table:
+    """Opaque table handle (python_binding.cu:194); only the parameter-server
+    tables derive from it in the reference, and those are not in this build."""
+
+
+# ---------------------------------------------------------------------------
+# layer bindings (binding_layers.hpp)
+# ---------------------------------------------------------------------------
+
+_ELEM = {DataType_t.Float32: 4, DataType_t.Float16: 2}
+
+
+class NVEmbedBinding:
+    """Common surface of the layer bindings (binding_layers.hpp:67-408)."""
+
+    def __init__(self, device_id, row_size, dtype, config):
+        self.device_id_ = int(device_id)
+        self.data_type_ = DataType_t(dtype)
+        # binding_layers.hpp:306-307: 4-byte elements for Float32, 2 otherwise
+        self.row_size_in_bytes_ = int(row_size) * (4 if self.data_type_ == DataType_t.Float32 else 2)
+        self.logging_interval_ = int(config.logging_interval) if config is not None else -1
+        self.logging_counter_ = 0
+        self._layer = None
+        self._contexts = {}
+        self._ctx_mu = threading.Lock()
+        self._modify_stream = None
+        if self.device_id_ >= 0:
+            import torch
+            self._modify_stream = torch.cuda.Stream(device=self.device_id_)
+
+    # accessors used by the torch ops (binding_layers.hpp:71-84)
+    def get_embedding_dim(self):
+        if self.data_type_ not in _ELEM:
+            raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, "Invalid data type")
+        return self.row_size_in_bytes_ // _ELEM[self.data_type_]
+
+    def get_data_type(self):
+        return self.data_type_
+
+    def _ctx(self, stream):
+        stream = int(stream or 0)
+        with self._ctx_mu:
+            ctx = self._contexts.get(stream)
+            if ctx is None:
+                h = ctypes.c_void_p()
+                modify = self._modify_stream.cuda_stream if self._modify_stream is not None else 0
+                _lib.call("nve_layer_create_execution_context", self._layer, ctypes.byref(h),
+                          ctypes.c_void_p(stream), ctypes.c_void_p(modify), None, None)
+                ctx = self._contexts[stream] = h.value
+            return ctx
+
+    def _log_hit_rates(self, hr):
+        if self.logging_interval_ > 0:
+            if self.logging_counter_ % self.logging_interval_ == 0:
+                _log.info("Hit rates: %s", ", ".join(str(v) for v in hr))
+            self.logging_counter_ += 1
+
+    def lookup(self, num_keys, keys, output, stream):
+        """One output row per key (binding_layers.hpp:86-101)."""
+        hr = (ctypes.c_float * 3)()
+        ctx = self._ctx(stream)
+        _lib.call("nve_layer_lookup", self._layer, ctx, int(num_keys), ctypes.c_void_p(keys),
+                  ctypes.c_void_p(output), self.row_size_in_bytes_, None, hr)
+        self._log_hit_rates(list(hr))
+
+    def lookup_with_pooling(self, num_keys, keys, output, pooling_type, num_offsets, offsets,
+                            weight_data_type, weights, stream):
+        """CSR-pooled lookup, output in the table's dtype (binding_layers.hpp:103-129)."""
+        hr = (ctypes.c_float * 3)()
+        ctx = self._ctx(stream)
+        _lib.call("nve_layer_lookup_pooled", self._layer, ctx, int(num_keys), ctypes.c_void_p(keys),
+                  ctypes.c_void_p(output), self.row_size_in_bytes_, None, int(pooling_type),
+                  _lib.SPARSE_CSR, ctypes.c_void_p(offsets), int(num_offsets), 0,
+                  ctypes.c_void_p(weights), int(weight_data_type), int(self.data_type_), hr)
+        self._log_hit_rates(list(hr))
+
+    def insert(self, num_keys, keys, values, table_id, stream):
+        ctx = self._ctx(stream)
+        _lib.call("nve_layer_insert", self._layer, ctx, int(num_keys), ctypes.c_void_p(keys),
+                  self.row_size_in_bytes_, self.row_size_in_bytes_, ctypes.c_void_p(values),
+                  int(table_id))
+
+    def update(self, num_keys, keys, updates, stream):
+        ctx = self._ctx(stream)
+        _lib.call("nve_layer_update", self._layer, ctx, int(num_keys), ctypes.c_void_p(keys),
+                  self.row_size_in_bytes_, self.row_size_in_bytes_, ctypes.c_void_p(updates), -1)
+
+    def accumulate(self, num_keys, keys, updates, stream):
+        ctx = self._ctx(stream)
+        _lib.call("nve_layer_accumulate", self._layer, ctx, int(num_keys), ctypes.c_void_p(keys),
+                  self.row_size_in_bytes_, self.row_size_in_bytes_, ctypes.c_void_p(updates),
+                  int(self.data_type_), -1)
+
+    def clear(self, stream):
+        _lib.call("nve_layer_clear", self._layer, self._ctx(stream))
+
+    def erase(self, num_keys, keys, table_id, stream):
+        _lib.call("nve_layer_erase", self._layer, self._ctx(stream), int(num_keys),
+                  ctypes.c_void_p(keys), int(table_id))
+
+    def concat_backprop(self, *args):
+        _not_in_build("Gradient computation (concat_backprop)")
+
+    def pooling_backprop(self, *args):
+        _not_in_build("Gradient computation (pooling_backprop)")
+
+    def get_num_tables(self):
+        out = ctypes.c_int64()
+        _lib.call("nve_layer_get_num_tables", self._layer, ctypes.byref(out))
+        return out.value
+
+    def release_contexts(self):
+        """Wait for and destroy every context (binding_layers.hpp:339-350)."""
+        with self._ctx_mu:
+            for ctx in self._contexts.values():
+                _lib.call("nve_context_wait", ctx)
+                _lib.call("nve_context_destroy", ctx)
+            self._contexts.clear()
+
+    def _destroy(self):
+        if getattr(self, "_layer", None) is None or _lib._lib is None:
+            return
+        try:
+            self.release_contexts()
+        finally:
+            _lib._lib.nve_layer_destroy(self._layer)
+            self._layer = None
+
+    def __del__(self):
+        self._destroy()
+
+
+class GPUEmbedding(NVEmbedBinding):
+    """Linear table in GPU memory, no cache (binding_layers.hpp:660-728)."""
+
+    def __init__(self, row_size, num_embeddings, dtype, mem_block, device_id, config=None):
+        config = config if config is not None else EmbedLayerConfig()
+        super().__init__(device_id, row_size, dtype, config)
+        self.num_embeddings_ = int(num_embeddings)
+        self.mem_block_ = mem_block
+        cfg = _lib.load().nve_gpu_embedding_layer_config_default()
+        cfg.layer_name = b"gpu_layer"
+        cfg.device_id = self.device_id_
+        cfg.embedding_table = mem_block.get_ptr()
+        cfg.num_embeddings = self.num_embeddings_
+        cfg.embedding_width_in_bytes = self.row_size_in_bytes_
+        cfg.value_dtype = int(self.data_type_)
+        cfg.default_row_index = int(config.default_row_index)
+        h = ctypes.c_void_p()
+        _lib.call("nve_gpu_embedding_layer_create", ctypes.byref(h), _lib.KEY_INT64,
+                  ctypes.byref(cfg), None)
+        self._layer = h.value
+
+
+class LinearUVMEmbedding(NVEmbedBinding):
+    """GPU cache in front of a host-resident linear table
+    (binding_layers.hpp:529-657)."""
+
+    def __init__(self, row_size, num_embeddings, dtype, mem_block, gpu_cache_size,
+                 use_private_stream, device_id, config=None):
+        config = config if config is not None else EmbedLayerConfig()
+        super().__init__(device_id, row_size, dtype, config)
+        self.num_embeddings_ = int(num_embeddings)
+        self.mem_block_ = mem_block
+        self.row_size_ = int(row_size)
+        self._table = None
+        self._private_stream = None
+        cfg = _lib.load().nve_gpu_table_config_default()
+        cfg.device_id = self.device_id_
+        cfg.cache_size = int(gpu_cache_size)
+        cfg.row_size_in_bytes = self.row_size_in_bytes_
+        cfg.value_dtype = int(self.data_type_)
+        cfg.count_misses = 1
+        if config.max_modify_size > 0:
+            cfg.max_modify_size = int(config.max_modify_size)
+        if use_private_stream:
+            import torch
+            self._private_stream = torch.cuda.Stream(device=self.device_id_)
+            cfg.private_stream = self._private_stream.cuda_stream
+        cfg.uvm_table = mem_block.get_ptr()
+        cfg.uvm_num_rows = self.num_embeddings_
+        # kernel modes (binding_layers.hpp:565-576) are recorded; one fused
+        # hit/miss kernel serves all of them in this build
+        cfg.kernel_mode_type = int(config.kernel_mode)
+        if config.kernel_mode == 1:  # SortGather: minimum key count
+            cfg.kernel_mode_value = int(config.kernel_mode_value_1) if config.kernel_mode_value_1 > 0 else 1024
+        t = ctypes.c_void_p()
+        _lib.call("nve_gpu_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(cfg), None)
+        self._table = t.value
+        try:
+            lcfg = _lib.load().nve_linear_uvm_layer_config_default()
+            lcfg.layer_name = b"uvm_layer"
+            lcfg.default_row_index = int(config.default_row_index)
+            h = ctypes.c_void_p()
+            _lib.call("nve_linear_uvm_layer_create", ctypes.byref(h), _lib.KEY_INT64,
+                      ctypes.byref(lcfg), self._table, None)
+            self._layer = h.value
+        except Exception:
+            _lib._lib.nve_table_destroy(self._table)
+            self._table = None
+            raise
+
+    def get_table_tensor(self):
+        """The backing table as a [num_embeddings, row_size] host tensor that
+        shares the block's memory (the reference hands out a DLPack view,
+        binding_layers.hpp:588-617)."""
+        import torch
+        tdt = torch.float32 if self.data_type_ == DataType_t.Float32 else torch.float16
+        n = self.num_embeddings_ * self.row_size_
+        if n == 0:
+            return torch.empty((self.num_embeddings_, self.row_size_), dtype=tdt)
+        buf = (ctypes.c_char * (n * tdt.itemsize)).from_address(self.mem_block_.get_ptr())
+        t = torch.frombuffer(buf, dtype=tdt).view(self.num_embeddings_, self.row_size_)
+        t._nve_owner = self  # keep the binding (and its memory block) alive
+        return t
+
+    def _destroy(self):
+        try:
+            super()._destroy()
+        finally:
+            if getattr(self, "_table", None) is not None and _lib._lib is not None:
+                if self._private_stream is not None:
+                    self._private_stream.synchronize()
+                _lib._lib.nve_table_destroy(self._table)
+                self._table = None
+
+
+class HostEmbedding(NVEmbedBinding):
+    def __init__(self, *args, **kwargs):
+        _not_in_build("HostEmbedding (the CPU host layer)")
+
+
+class HierarchicalEmbedding(NVEmbedBinding):
+    def __init__(self, *args, **kwargs):
+        _not_in_build("HierarchicalEmbedding (host / remote tiers)")
+
+
+def get_dl_tensor(layer, dtype=None):
+    """View of a LinearUVMEmbedding's backing table (python_binding.cu:65-81);
+    a torch tensor, which `torch.utils.dlpack.from_dlpack` accepts as is."""
+    if not isinstance(layer, LinearUVMEmbedding):
+        raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, "get_dl_tensor takes a LinearUVMEmbedding")
+    return layer.get_table_tensor()
+
+
+# ---------------------------------------------------------------------------
+# marker-tensor registry of the torch ops (nve_registry.cu:25-50)
+# ---------------------------------------------------------------------------
+
+_registry = {}
+_registry_mu = threading.Lock()
+
+
+def register_for_torch(marker_ptr, binding):
+    with _registry_mu:
+        _registry[int(marker_ptr)] = binding
+
+
+def unregister_from_torch(marker_ptr):
+    with _registry_mu:
+        _registry.pop(int(marker_ptr), None)
+
+
+def get_binding(marker_ptr):
+    with _registry_mu:
+        b = _registry.get(int(marker_ptr))
+    if b is None:
+        raise RuntimeError(f"NVELayerRegistry: no binding registered for marker_ptr={int(marker_ptr):#x}")
+    return b
