@@ -30,7 +30,9 @@ enum {
  * Restates the reference's kernel-level router find_and_pool
  * (cuda_ops/find_and_pool.cuh:103-132) with a linear table
  * (ECNoCache, load_indices = true): Concatenate emits one dequantized row per
- * key, every other pooling type one fp32-accumulated row per bag.
+ * key, every other pooling type one fp32-accumulated row per bag.  Keys
+ * outside [0, num_rows) read nothing: their Concatenate output rows are left
+ * as they are, and a bag counts them as zero rows.
  * output_type: the value type's float precision (either precision for the
  * extension types).  split_hint: 0 lets the library choose how many lane
  * groups share a bag; > 0 forces that many (a power of two); < 0 forces one

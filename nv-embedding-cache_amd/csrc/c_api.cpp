@@ -662,6 +662,7 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
   src.table = static_cast<const uint8_t*>(table);
   src.row_bytes = (uint64_t)row_size_in_bytes;
   src.load_indices = 1;
+  src.num_rows = (uint64_t)num_rows;
   if (pooling_type == NVE_POOL_CONCATENATE) {
     GatherLaunch g{};
     g.keys = keys;

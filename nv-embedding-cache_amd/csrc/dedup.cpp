@@ -78,7 +78,7 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   const uint64_t* ks = alt ? b.kb : b.ka;
   const uint32_t* vs = alt ? b.vb : b.va;
   NVE_HIP(launch_run_heads(ks, n, b.heads, s));
-  NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, s));
+  NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, b.sort_tmp, s));
   NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, s));
   uint32_t u = 0;
   NVE_HIP(hipMemcpyAsync(&u, b.total, sizeof(u), hipMemcpyDeviceToHost, s));

@@ -69,58 +69,78 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
 
 // ---------------------------------------------------------------------------
 // vector loads / stores of VB bytes (VB in {1,2,4,8,16}, address VB-aligned)
+//
+// Row addresses are computed integers, so the accesses go through pointers in
+// the global address space: they become global_load / global_store, which
+// count only against vmcnt.  (Generic pointers would give flat accesses that
+// also count against lgkmcnt, so every wait for a lane shuffle would drain the
+// row loads in flight as well.)
 // ---------------------------------------------------------------------------
+template <typename T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+using gptr_w = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ T gload(uint64_t addr) {
+  return *reinterpret_cast<gptr<T>>(addr);
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// VB bytes as 32-bit words (the low bytes of w[0] for VB < 4); element e of
+// an ES-byte type is bits [8*ES*(e % (4/ES)), ...) of word e / (4/ES).
 template <int VB>
 struct Vec {
-  uint8_t b[VB];
+  uint32_t w[VB >= 4 ? VB / 4 : 1];
 };
 
 template <int VB>
-__device__ __forceinline__ Vec<VB> load_vec(const uint8_t* p) {
+__device__ __forceinline__ Vec<VB> load_vec(uint64_t addr) {
   Vec<VB> v;
   if constexpr (VB == 16) {
-    const uint4 x = *reinterpret_cast<const uint4*>(p);
-    __builtin_memcpy(v.b, &x, 16);
+    const u32x4 x = gload<u32x4>(addr);
+    v.w[0] = x.x;
+    v.w[1] = x.y;
+    v.w[2] = x.z;
+    v.w[3] = x.w;
   } else if constexpr (VB == 8) {
-    const uint2 x = *reinterpret_cast<const uint2*>(p);
-    __builtin_memcpy(v.b, &x, 8);
+    const u32x2 x = gload<u32x2>(addr);
+    v.w[0] = x.x;
+    v.w[1] = x.y;
   } else if constexpr (VB == 4) {
-    const uint32_t x = *reinterpret_cast<const uint32_t*>(p);
-    __builtin_memcpy(v.b, &x, 4);
+    v.w[0] = gload<uint32_t>(addr);
   } else if constexpr (VB == 2) {
-    const uint16_t x = *reinterpret_cast<const uint16_t*>(p);
-    __builtin_memcpy(v.b, &x, 2);
+    v.w[0] = gload<uint16_t>(addr);
   } else {
-    v.b[0] = *p;
+    v.w[0] = gload<uint8_t>(addr);
   }
   return v;
+}
+template <int VB>
+__device__ __forceinline__ Vec<VB> load_vec(const uint8_t* p) {
+  return load_vec<VB>((uint64_t)p);
+}
+
+__device__ __forceinline__ uint32_t vbyte(const uint32_t* w, int e) {
+  return (w[e >> 2] >> ((e & 3) * 8)) & 0xffu;
+}
+__device__ __forceinline__ uint16_t vhalf(const uint32_t* w, int e) {
+  return (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
 }
 
 // Streaming store (the output is written once and not re-read by the lookup).
 template <int VB>
 __device__ __forceinline__ void store_vec(uint8_t* p, const Vec<VB>& v) {
-  if constexpr (VB == 16) {
-    uint4 x;
-    __builtin_memcpy(&x, v.b, 16);
-    __builtin_nontemporal_store(x.x, reinterpret_cast<uint32_t*>(p) + 0);
-    __builtin_nontemporal_store(x.y, reinterpret_cast<uint32_t*>(p) + 1);
-    __builtin_nontemporal_store(x.z, reinterpret_cast<uint32_t*>(p) + 2);
-    __builtin_nontemporal_store(x.w, reinterpret_cast<uint32_t*>(p) + 3);
-  } else if constexpr (VB == 8) {
-    uint2 x;
-    __builtin_memcpy(&x, v.b, 8);
-    __builtin_nontemporal_store(x.x, reinterpret_cast<uint32_t*>(p) + 0);
-    __builtin_nontemporal_store(x.y, reinterpret_cast<uint32_t*>(p) + 1);
-  } else if constexpr (VB == 4) {
-    uint32_t x;
-    __builtin_memcpy(&x, v.b, 4);
-    __builtin_nontemporal_store(x, reinterpret_cast<uint32_t*>(p));
+  const uint64_t a = (uint64_t)p;
+  if constexpr (VB >= 4) {
+#pragma unroll
+    for (int i = 0; i < VB / 4; ++i)
+      __builtin_nontemporal_store(v.w[i], reinterpret_cast<gptr_w<uint32_t>>(a) + i);
   } else if constexpr (VB == 2) {
-    uint16_t x;
-    __builtin_memcpy(&x, v.b, 2);
-    *reinterpret_cast<uint16_t*>(p) = x;
+    *reinterpret_cast<gptr_w<uint16_t>>(a) = (uint16_t)v.w[0];
   } else {
-    *p = v.b[0];
+    *reinterpret_cast<gptr_w<uint8_t>>(a) = (uint8_t)v.w[0];
   }
 }
 
@@ -129,22 +149,26 @@ template <int E>
 __device__ __forceinline__ void store_out(uint8_t* p, const float* v, bool out_f16) {
   if (out_f16) {
     Vec<2 * E> o;
+    if constexpr (E == 1) {
+      o.w[0] = f2h(v[0]);
+    } else {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const uint16_t h = f2h(v[e]);
-      __builtin_memcpy(o.b + 2 * e, &h, 2);
+      for (int i = 0; i < E / 2; ++i)
+        o.w[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
     }
     store_vec<2 * E>(p, o);
   } else {
     if constexpr (E <= 4) {
       Vec<4 * E> o;
-      __builtin_memcpy(o.b, v, 4 * E);
+#pragma unroll
+      for (int i = 0; i < E; ++i) o.w[i] = __float_as_uint(v[i]);
       store_vec<4 * E>(p, o);
     } else {
 #pragma unroll
       for (int c = 0; c < E / 4; ++c) {
         Vec<16> o;
-        __builtin_memcpy(o.b, v + 4 * c, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint(v[4 * c + i]);
         store_vec<16>(p + 16 * c, o);
       }
     }
@@ -207,8 +231,8 @@ struct Meta {
 // Metadata sits right after the value area; its address is only 2-byte
 // aligned in general, so it is assembled from 16-bit loads.
 __device__ __forceinline__ float ld_f32_unaligned(const uint8_t* p) {
-  const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
-  const uint32_t v = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+  const uint64_t a = (uint64_t)p;
+  const uint32_t v = (uint32_t)gload<uint16_t>(a) | ((uint32_t)gload<uint16_t>(a + 2) << 16);
   return __uint_as_float(v);
 }
 
@@ -222,10 +246,10 @@ __device__ __forceinline__ Meta load_meta(const uint8_t* row, int64_t value_byte
     m.s = ld_f32_unaligned(p);
     m.o = ld_f32_unaligned(p + 4);
   } else if constexpr (SDT == kQI8F16) {
-    m.s = h2f(*reinterpret_cast<const uint16_t*>(p));
+    m.s = h2f(gload<uint16_t>((uint64_t)p));
   } else if constexpr (SDT == kQU8F16) {
-    m.s = h2f(*reinterpret_cast<const uint16_t*>(p));
-    m.o = h2f(*reinterpret_cast<const uint16_t*>(p + 2));
+    m.s = h2f(gload<uint16_t>((uint64_t)p));
+    m.o = h2f(gload<uint16_t>((uint64_t)p + 2));
   }
   return m;
 }
@@ -245,24 +269,20 @@ __device__ __forceinline__ void decode(const Vec<VB>& v, const Meta& m,
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     if constexpr (SDT == kF32) {
-      float f;
-      __builtin_memcpy(&f, v.b + 4 * e, 4);
-      x[e] = f;
+      x[e] = __uint_as_float(v.w[e]);
     } else if constexpr (SDT == kF16) {
-      uint16_t h;
-      __builtin_memcpy(&h, v.b + 2 * e, 2);
-      x[e] = h2f(h);
+      x[e] = h2f(vhalf(v.w, e));
     } else if constexpr (SDT == kQI8F32) {
-      x[e] = __builtin_fmaf((float)(int8_t)v.b[e], m.s, 0.0f);
+      x[e] = __builtin_fmaf((float)(int8_t)vbyte(v.w, e), m.s, 0.0f);
     } else if constexpr (SDT == kQU8F32 || SDT == kXI8AF32) {
-      const float q = (SDT == kQU8F32) ? (float)v.b[e] : (float)(int8_t)v.b[e];
+      const float q = (SDT == kQU8F32) ? (float)vbyte(v.w, e) : (float)(int8_t)vbyte(v.w, e);
       x[e] = __builtin_fmaf(q, m.s, m.o);
     } else if constexpr (SDT == kQI8F16) {
-      x[e] = h2f(f2h((float)(int8_t)v.b[e] * m.s));
+      x[e] = h2f(f2h((float)(int8_t)vbyte(v.w, e) * m.s));
     } else if constexpr (SDT == kQU8F16) {
-      x[e] = h2f(f2h(__builtin_fmaf((float)v.b[e], m.s, m.o)));
+      x[e] = h2f(f2h(__builtin_fmaf((float)vbyte(v.w, e), m.s, m.o)));
     } else if constexpr (SDT == kXE4M3F32) {
-      x[e] = e4m3_to_f32(v.b[e]) * m.s;
+      x[e] = e4m3_to_f32((uint8_t)vbyte(v.w, e)) * m.s;
     }
   }
 }

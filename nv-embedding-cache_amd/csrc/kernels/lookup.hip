@@ -117,6 +117,13 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
   }
 }
 
+// Readable zeros for keys that resolve to no row: their loads are pointed
+// here (offsets folded into the buffer) so that every load of a batch can be
+// issued unconditionally.
+constexpr int kZeroRowBytes = 4096;
+constexpr int64_t kZeroRowMask = kZeroRowBytes - 1;
+__device__ __align__(16) uint8_t g_zero_row[kZeroRowBytes + 64] = {};
+
 // ---------------------------------------------------------------------------
 // find-and-pool: one output row per bag
 // ---------------------------------------------------------------------------
@@ -172,6 +179,7 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
 
   const bool weighted = a.weighted != 0;
   const int64_t value_bytes = a.count * ES;
+  const uint64_t zero_row = (uint64_t)g_zero_row;
   const bool out_f16 = a.out_dtype == kF16;
   const int out_es = out_f16 ? 2 : 4;
   uint32_t misses = 0;
@@ -198,33 +206,41 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
       }
       const int n = (int)((ce - k0) < G ? (ce - k0) : G);
       for (int j0 = 0; j0 < n; j0 += U) {
+        // (1) the batch's row addresses (and weights) from the lanes that
+        // resolved them; slots past the group's keys repeat its last key
+        uint64_t ra[U];
+        float wu[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = (j0 + u < n) ? j0 + u : n - 1;
+          ra[u] = shfl64(addr, gbase + j);
+          wu[u] = weighted ? shflf(w, gbase + j) : 1.0f;
+        }
+        // (2) every row load of the batch in flight at once; a key that did
+        // not resolve (outside the table) reads the zero row instead
         Vec<VB> v[U];
         Meta m[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int j = (j0 + u < n) ? j0 + u : n - 1;
-          const uint64_t ra = shfl64(addr, gbase + j);
-          if (j0 + u < n) {
-            if (in_row) v[u] = load_vec<VB>(reinterpret_cast<const uint8_t*>(ra) + off);
-            if constexpr (Fmt<SDT>::meta != 0)
-              m[u] = load_meta<SDT>(reinterpret_cast<const uint8_t*>(ra), value_bytes);
-          }
+          const bool real = ra[u] != 0;
+          const uint64_t row = real ? ra[u] : zero_row;
+          v[u] = load_vec<VB>(row + ((real && in_row) ? off : (off & kZeroRowMask)));
+          if constexpr (Fmt<SDT>::meta != 0)
+            m[u] = load_meta<SDT>(reinterpret_cast<const uint8_t*>(row),
+                                  real ? value_bytes : (value_bytes & kZeroRowMask));
         }
+        // (3) accumulate in key order; an unresolved key adds a zero row
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          if (j0 + u < n) {  // uniform over the group
-            float wu = 1.0f;
-            if (weighted) {
-              wu = shflf(w, gbase + j0 + u);
-              wsum += wu;
-            }
-            if (in_row) {
-              float x[E];
-              decode<SDT, VB>(v[u], m[u], x);
+          const bool use = j0 + u < n;  // uniform over the group
+          if (weighted && use) wsum += wu[u];
+          const bool add = use && in_row && ra[u] != 0;
+          float x[E];
+          decode<SDT, VB>(v[u], m[u], x);
 #pragma unroll
-              for (int c = 0; c < E; ++c)
-                acc[c] = weighted ? __builtin_fmaf(x[c], wu, acc[c]) : acc[c] + x[c];
-            }
+          for (int c = 0; c < E; ++c) {
+            const float t = weighted ? __builtin_fmaf(x[c], wu[u], acc[c]) : acc[c] + x[c];
+            acc[c] = add ? t : acc[c];
           }
         }
       }
@@ -359,13 +375,13 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const uint8_t* table,
     r[u] = i < n ? idx[i] : -1;
   }
   for (int c = gl; c < vecs; c += 16) {
-    uint4 v[8];
+    Vec<16> v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (r[u] >= 0) v[u] = reinterpret_cast<const uint4*>(table + (uint64_t)r[u] * row_bytes)[c];
+      v[u] = load_vec<16>((uint64_t)table + (uint64_t)(r[u] >= 0 ? r[u] : 0) * row_bytes + 16 * c);
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (r[u] >= 0) fold ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+      if (r[u] >= 0) fold ^= v[u].w[0] ^ v[u].w[1] ^ v[u].w[2] ^ v[u].w[3];
   }
   __shared__ uint32_t red[256];
   red[threadIdx.x] = fold;

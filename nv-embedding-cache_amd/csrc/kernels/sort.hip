@@ -9,21 +9,31 @@
 // expressed by the caller as ascending sorts of a complemented key).
 //
 // One pass per 8-bit digit, three kernels per pass:
-//   hist     each 256-thread workgroup counts the digits of its 2048-key tile
+//   hist     each 256-thread workgroup counts the digits of its 1024-key tile
 //            into LDS and writes the 256 counts digit-major;
-//   scan     one workgroup turns the digit-major counts into exclusive offsets
-//            (digit d of tile t lands after every smaller digit and after
-//            digit d of tiles < t: this is what makes the pass stable);
-//   scatter  each workgroup ranks its keys stably: a wave finds the lanes
-//            sharing its digit with eight ballots, ranks by popcount of the
-//            lower lanes, and adds the counts of earlier waves and rounds.
+//   rowscan  one workgroup per digit turns its row of per-tile counts into
+//            exclusive prefixes (a separate array) and writes the digit's total;
+//   scatter  each workgroup scans the 256 digit totals (digit d starts after
+//            every smaller digit) and adds its tile's row prefix (digit d of
+//            tile t lands after digit d of tiles < t: this is what makes the
+//            pass stable).  It ranks its keys stably inside the tile -- a wave
+//            finds the lanes sharing its digit with eight ballots, ranks by
+//            popcount of the lower lanes, and adds the counts of earlier waves
+//            and rounds -- stages the tile in LDS in digit order, and writes
+//            it out so that consecutive threads store consecutive positions of
+//            a digit's run.
+//
+// The exclusive scan of an array (run heads in dedup and insert) is
+// reduce-then-scan over 4096-element blocks: block sums, a scan of the sums
+// (recursively, in the caller's temporary storage), then each block rescans
+// its elements from its offset.
 #include "device_common.cuh"
 #include "sort_launch.hpp"
 
 namespace nve_amd {
 
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 8;
+constexpr int kSortItems = 4;
 constexpr int kSortTile = kSortThreads * kSortItems;
 
 __global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, int64_t n, int shift,
@@ -42,77 +52,195 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, i
   counts[(int64_t)tid * nblocks + blockIdx.x] = h[tid];
 }
 
-// Exclusive scan of m uint32 in place by one 1024-thread workgroup: thread t
-// owns a contiguous chunk, chunks are summed, the chunk sums scanned in LDS,
-// then each chunk rewritten with its running prefix.  Also writes the total.
-__global__ __launch_bounds__(1024) void scan_kernel(uint32_t* data, int64_t m, uint32_t* total) {
-  __shared__ uint32_t sums[1024];
-  const int tid = threadIdx.x;
-  const int64_t chunk = (m + 1023) / 1024;
-  const int64_t b = tid * chunk;
-  const int64_t e = b + chunk < m ? b + chunk : m;
-  uint32_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += data[i];
-  sums[tid] = s;
+// Inclusive scan across the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = shfl32(v, lane >= o ? lane - o : lane);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan of one value per thread over a workgroup of NT threads
+// (NT a multiple of 64, at most 4096); `total` receives the sum.  `lds` holds
+// NT / 64 + 1 words; every thread of the workgroup must call it.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* lds,
+                                                         uint32_t* total) {
+  constexpr int kWaves = NT / 64;
+  const int lane = lane_id();
+  const int wave = (int)threadIdx.x >> 6;
+  const uint32_t inc = wave_inclusive_scan(v);
+  if (lane == 63) lds[wave] = inc;
   __syncthreads();
-  // Hillis-Steele inclusive scan of the 1024 chunk sums
-  for (int o = 1; o < 1024; o <<= 1) {
-    const uint32_t v = tid >= o ? sums[tid - o] : 0u;
-    __syncthreads();
-    sums[tid] += v;
-    __syncthreads();
+  if (threadIdx.x < 64) {
+    const uint32_t w = (int)threadIdx.x < kWaves ? lds[threadIdx.x] : 0u;
+    const uint32_t wi = wave_inclusive_scan(w);
+    if ((int)threadIdx.x < kWaves) lds[threadIdx.x] = wi - w;
+    if ((int)threadIdx.x == kWaves - 1) lds[kWaves] = wi;
   }
-  uint32_t run = tid > 0 ? sums[tid - 1] : 0u;
-  for (int64_t i = b; i < e; ++i) {
-    const uint32_t v = data[i];
-    data[i] = run;
-    run += v;
+  __syncthreads();
+  const uint32_t res = inc - v + lds[wave];
+  *total = lds[kWaves];
+  __syncthreads();
+  return res;
+}
+
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanBlock = kScanThreads * kScanItems;
+
+// Sum of each 4096-element block.
+__global__ __launch_bounds__(256) void scan_reduce_kernel(const uint32_t* data, int64_t m,
+                                                          uint32_t* sums) {
+  __shared__ uint32_t lds[kScanThreads / 64 + 1];
+  const int64_t base = (int64_t)blockIdx.x * kScanBlock + (int64_t)threadIdx.x * kScanItems;
+  uint32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j)
+    if (base + j < m) s += data[base + j];
+  uint32_t total;
+  (void)block_exclusive_scan<kScanThreads>(s, lds, &total);
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// Exclusive scan of each block from its offset (sums[block], or 0 with a
+// single block); the last block writes the grand total.
+__global__ __launch_bounds__(256) void scan_down_kernel(uint32_t* data, int64_t m,
+                                                        const uint32_t* offsets, uint32_t* total) {
+  __shared__ uint32_t lds[kScanThreads / 64 + 1];
+  const int64_t base = (int64_t)blockIdx.x * kScanBlock + (int64_t)threadIdx.x * kScanItems;
+  uint32_t v[kScanItems];
+  uint32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    v[j] = base + j < m ? data[base + j] : 0u;
+    s += v[j];
   }
-  if (tid == 1023 && total != nullptr) *total = sums[1023];
+  uint32_t block_total;
+  uint32_t run = block_exclusive_scan<kScanThreads>(s, lds, &block_total);
+  const uint32_t off = offsets ? offsets[blockIdx.x] : 0u;
+  run += off;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    if (base + j < m) data[base + j] = run;
+    run += v[j];
+  }
+  if (total != nullptr && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0)
+    *total = off + block_total;
+}
+
+// Row d of the digit-major per-tile counts -> exclusive prefixes in offs;
+// totals[d] = the row's sum.  One workgroup per digit.
+__global__ __launch_bounds__(256) void radix_rowscan_kernel(const uint32_t* counts, uint32_t* offs,
+                                                            int nblocks, uint32_t* totals) {
+  __shared__ uint32_t lds[256 / 64 + 1];
+  const uint32_t* row = counts + (int64_t)blockIdx.x * nblocks;
+  uint32_t* orow = offs + (int64_t)blockIdx.x * nblocks;
+  uint32_t carry = 0;
+  for (int c = 0; c < nblocks; c += 256 * 4) {
+    const int b = c + (int)threadIdx.x * 4;
+    uint32_t v[4];
+    uint32_t s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = b + j < nblocks ? row[b + j] : 0u;
+      s += v[j];
+    }
+    uint32_t chunk_total;
+    uint32_t run = carry + block_exclusive_scan<256>(s, lds, &chunk_total);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (b + j < nblocks) orow[b + j] = run;
+      run += v[j];
+    }
+    carry += chunk_total;
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys, const uint32_t* vals,
                                                             uint64_t* ko, uint32_t* vo, int64_t n,
-                                                            int shift, const uint32_t* offsets,
-                                                            int nblocks) {
-  __shared__ uint32_t run[256];
-  __shared__ uint32_t wcnt[4][256];
+                                                            int shift, const uint32_t* counts,
+                                                            const uint32_t* offs,
+                                                            const uint32_t* totals, int nblocks) {
+  constexpr int kSlots = kSortItems * (kSortThreads / 64);  // (round, wave) pairs in key order
+  __shared__ uint64_t sk[kSortTile];
+  __shared__ uint32_t sv[kSortTile];
+  __shared__ uint32_t lstart[256];          // first local position of digit d in the tile
+  __shared__ uint32_t gbase[256];           // output position of that key
+  __shared__ uint32_t slot[kSlots][256];    // keys of digit d per (round, wave), then their prefix
+  __shared__ uint32_t lds[256 / 64 + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  run[tid] = offsets[(int64_t)tid * nblocks + blockIdx.x];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) wcnt[w][tid] = 0;
-  __syncthreads();
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  const int tile_n = (int)(n - base < kSortTile ? n - base : kSortTile);
+  // all of the tile's loads in flight at once
+  uint64_t k[kSortItems];
+  uint32_t v[kSortItems];
+#pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
-    const int64_t i = base + r * kSortThreads + tid;
-    const bool valid = i < n;
-    const uint64_t k = valid ? keys[i] : 0ull;
-    const uint32_t v = valid ? vals[i] : 0u;
-    const uint32_t d = (uint32_t)(k >> shift) & 255u;
+    const int li = r * kSortThreads + tid;
+    k[r] = li < tile_n ? keys[base + li] : 0ull;
+    v[r] = li < tile_n ? vals[base + li] : 0u;
+  }
+  const int64_t tile = (int64_t)tid * nblocks + blockIdx.x;
+  uint32_t all;
+  const uint32_t digit_base = block_exclusive_scan<256>(totals[tid], lds, &all);
+  const uint32_t local = block_exclusive_scan<256>(counts[tile], lds, &all);
+  lstart[tid] = local;
+  gbase[tid] = digit_base + offs[tile];
+#pragma unroll
+  for (int q = 0; q < kSlots; ++q) slot[q][tid] = 0;
+  __syncthreads();
+  // per (round, wave): lanes sharing the digit, rank among them, count by the leader
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint32_t rank[kSortItems];
+#pragma unroll
+  for (int r = 0; r < kSortItems; ++r) {
+    const bool valid = r * kSortThreads + tid < tile_n;
+    const uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const uint64_t m = __ballot((d >> b) & 1u);
       peers &= ((d >> b) & 1u) ? m : ~m;
     }
-    const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
-    const bool leader = valid && (peers & lt_mask) == 0;
-    if (leader) wcnt[wave][d] = (uint32_t)__popcll(peers);
-    __syncthreads();
-    if (valid) {
-      uint32_t pos = run[d] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
-      ko[pos] = k;
-      vo[pos] = v;
-    }
-    __syncthreads();
-    run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+    rank[r] = (uint32_t)__popcll(peers & lt_mask);
+    if (valid && rank[r] == 0) slot[r * (kSortThreads / 64) + wave][d] = (uint32_t)__popcll(peers);
+  }
+  __syncthreads();
+  // thread d: exclusive prefix of digit d over the slots, from its local start
+  {
+    uint32_t acc = lstart[tid];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) wcnt[w][tid] = 0;
-    __syncthreads();
+    for (int q = 0; q < kSlots; ++q) {
+      const uint32_t c = slot[q][tid];
+      slot[q][tid] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortItems; ++r) {
+    if (r * kSortThreads + tid < tile_n) {
+      const uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
+      const uint32_t pos = slot[r * (kSortThreads / 64) + wave][d] + rank[r];
+      sk[pos] = k[r];
+      sv[pos] = v[r];
+    }
+  }
+  __syncthreads();
+  // the tile in digit order: runs of one digit go to consecutive positions
+  for (int j = tid; j < tile_n; j += kSortThreads) {
+    const uint64_t kk = sk[j];
+    const uint32_t d = (uint32_t)(kk >> shift) & 255u;
+    const uint32_t pos = gbase[d] + (uint32_t)j - lstart[d];
+    ko[pos] = kk;
+    vo[pos] = sv[j];
   }
 }
 
@@ -130,9 +258,19 @@ __global__ __launch_bounds__(256) void key_span_kernel(const uint64_t* keys, int
 }
 
 // ---------------------------------------------------------------------------
+size_t scan_temp_bytes(int64_t m) {
+  // block sums of every level of the recursion, each level 256-byte aligned
+  size_t bytes = 0;
+  for (int64_t nb = (m + kScanBlock - 1) / kScanBlock; nb > 1; nb = (nb + kScanBlock - 1) / kScanBlock)
+    bytes += ((size_t)nb * sizeof(uint32_t) + 255) / 256 * 256;
+  return bytes;
+}
+
 size_t radix_sort_temp_bytes(int64_t n) {
   const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
-  return (size_t)(nblocks > 0 ? nblocks : 1) * 256 * sizeof(uint32_t) + 256;
+  const size_t sort = (size_t)(nblocks > 0 ? nblocks : 1) * 256 * sizeof(uint32_t) * 2 + 1024;
+  const size_t scan = scan_temp_bytes(n);
+  return sort > scan ? sort : scan;
 }
 
 hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
@@ -143,6 +281,8 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
   if (nblocks > 0x7fffffff) return hipErrorInvalidValue;
   uint32_t* counts = static_cast<uint32_t*>(temp);
+  uint32_t* offs = counts + nblocks * 256;
+  uint32_t* totals = offs + nblocks * 256;
   uint64_t* ki = keys;
   uint32_t* vi = vals;
   uint64_t* ka = keys_alt;
@@ -150,10 +290,10 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   for (int shift = begin_bit; shift < end_bit; shift += 8) {
     hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
                        shift, counts, (int)nblocks);
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, counts, nblocks * 256,
-                       (uint32_t*)nullptr);
+    hipLaunchKernelGGL(radix_rowscan_kernel, dim3(256), dim3(256), 0, stream, counts, offs,
+                       (int)nblocks, totals);
     hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, vi,
-                       ka, va, n, shift, counts, (int)nblocks);
+                       ka, va, n, shift, counts, offs, totals, (int)nblocks);
     std::swap(ki, ka);
     std::swap(vi, va);
     *result_in_alt ^= 1;
@@ -161,9 +301,23 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   return hipGetLastError();
 }
 
-hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, hipStream_t stream) {
+hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, void* temp,
+                              hipStream_t stream) {
   if (m <= 0) return hipSuccess;
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, data, m, total);
+  const int64_t nb = (m + kScanBlock - 1) / kScanBlock;
+  if (nb > 0x7fffffff) return hipErrorInvalidValue;
+  if (nb == 1) {
+    hipLaunchKernelGGL(scan_down_kernel, dim3(1), dim3(kScanThreads), 0, stream, data, m,
+                       (const uint32_t*)nullptr, total);
+    return hipGetLastError();
+  }
+  uint32_t* sums = static_cast<uint32_t*>(temp);
+  void* rest = static_cast<uint8_t*>(temp) + ((size_t)nb * sizeof(uint32_t) + 255) / 256 * 256;
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, stream, data, m, sums);
+  hipError_t e = exclusive_scan_u32(sums, nb, nullptr, rest, stream);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(scan_down_kernel, dim3(nb), dim3(kScanThreads), 0, stream, data, m, sums,
+                     total);
   return hipGetLastError();
 }
 

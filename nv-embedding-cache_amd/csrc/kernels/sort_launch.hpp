@@ -8,8 +8,11 @@
 
 namespace nve_amd {
 
-// Bytes of temporary storage radix_sort_pairs needs for n pairs.
+// Bytes of temporary storage radix_sort_pairs needs for n pairs; it also
+// covers exclusive_scan_u32 of up to n elements.
 size_t radix_sort_temp_bytes(int64_t n);
+// Bytes of temporary storage exclusive_scan_u32 needs for m elements.
+size_t scan_temp_bytes(int64_t m);
 
 // Stable ascending sort of (keys[i], vals[i]) on bits [begin_bit, end_bit) of
 // the keys (begin_bit a multiple of 8).  Ping-pongs between (keys, vals) and
@@ -18,8 +21,10 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
                             int64_t n, int begin_bit, int end_bit, void* temp, int* result_in_alt,
                             hipStream_t stream);
 
-// In-place exclusive scan of m uint32 (total, if non-null, gets the sum).
-hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, hipStream_t stream);
+// In-place exclusive scan of m uint32 (total, if non-null, gets the sum);
+// temp holds scan_temp_bytes(m) bytes.
+hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, void* temp,
+                              hipStream_t stream);
 
 // *out |= OR over i of (keys[i] ^ keys[0]); *out must start at 0.
 hipError_t key_span(const uint64_t* keys, int64_t n, unsigned long long* out, hipStream_t stream);

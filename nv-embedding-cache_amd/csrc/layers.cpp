@@ -176,6 +176,9 @@ void GPUEmbeddingLayer::lookup(ExecutionContext& ctx, int64_t num_keys, const vo
   src.table = static_cast<const uint8_t*>(cfg_.embedding_table);
   src.row_bytes = (uint64_t)width;
   src.load_indices = 1;
+  // keys outside the table (no default row configured) read nothing: the
+  // gather leaves their output rows alone and pooling adds a zero row
+  src.num_rows = (uint64_t)cfg_.num_embeddings;
 
   {
     std::lock_guard<std::mutex> lk(launch_mu_);

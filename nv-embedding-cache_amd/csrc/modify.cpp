@@ -136,7 +136,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   uint64_t* ks = alt ? kb : ka;
   uint32_t* vs = alt ? vb : va;
   NVE_HIP(launch_run_heads(ks, n, heads, s));
-  NVE_HIP(exclusive_scan_u32(heads, n, d_count, s));
+  NVE_HIP(exclusive_scan_u32(heads, n, d_count, sort_tmp, s));
   const uint32_t uniq = read_u32(d_count, s);
   NVE_HIP(launch_run_gather(ks, vs, heads, n, start, ukey, first, s));
   // sort the runs by count descending (stable: ties keep ascending key order)
@@ -163,7 +163,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   const uint64_t* sk = alt3 ? k3b : k3;
   const uint32_t* sv = alt3 ? v3b : v3;
   NVE_HIP(launch_run_heads(sk, m, start, s));  // start reused as head flags
-  NVE_HIP(exclusive_scan_u32(start, m, d_count, s));
+  NVE_HIP(exclusive_scan_u32(start, m, d_count, sort_tmp, s));
   const uint32_t nrs = read_u32(d_count, s);
   NVE_HIP(launch_set_gather(sk, start, m, rset, roff, s));
 

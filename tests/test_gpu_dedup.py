@@ -72,6 +72,14 @@ def test_dedup_random(n, hi):
     check_against_oracle(keys)
 
 
+def test_dedup_multi_level_scans():
+    """4096 * 4096 + 3001 keys: the run-head scan recurses twice (more than
+    4096 blocks of 4096) and each radix digit row spans several 1024-tile
+    chunks."""
+    rng = np.random.default_rng(9)
+    check_against_oracle(rng.integers(-500, 1500, size=4096 * 4096 + 3001).astype(np.int64))
+
+
 def test_dedup_benchmark_zipf_keys_and_gather():
     """C2 shape: 262,144 Zipf(1.05) keys over 50M rows (reference generator),
     on a smaller table of the same row width (keys reduced modulo its rows)."""

@@ -146,3 +146,32 @@ def test_e4m3_every_code_decodes_exactly():
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.XI8A_F32])
+@pytest.mark.parametrize("split", [-1, 8])
+def test_out_of_range_keys_read_as_zero_rows(dtype, split):
+    """Keys outside [0, num_rows) add a zero row to their bag (and count in its
+    Mean); checked against the oracle on the table plus one zero row."""
+    rng = np.random.default_rng(21 + split)
+    rows, count, bags, hot = 500, 64, 12, 40
+    tb = (float_table(rng, rows, count, dtype, dyadic_values=False) if dtype == O.F16
+          else quant_table(rng, rows, count, dtype))
+    keys = rng.integers(0, rows, size=bags * hot).astype(np.int64)
+    bad = rng.random(keys.size) < 0.2
+    keys[bad] = rng.choice(np.array([-1, rows, rows + 7, 1 << 40, -(1 << 50)], np.int64), size=int(bad.sum()))
+    padded = np.concatenate([tb, np.zeros((1, tb.shape[1]), np.uint8)])
+    mapped = np.where((keys >= 0) & (keys < rows), keys, rows)
+    out_dtype = O.F16 if dtype == O.F16 else O.F32  # fp16 rows pool to fp16 (find_and_pool.cuh:40-51)
+    bits = np.uint16 if out_dtype == O.F16 else np.uint32
+    for pooling in (_lib.POOL_SUM, _lib.POOL_MEAN):
+        got = run_pool(tb, dtype, keys, pooling, _lib.SPARSE_FIXED, None, bags, hot, None, O.F32,
+                       out_dtype, split)
+        ref = oracle_pool(padded, mapped, dtype, count, O.FIXED, pooling, None, bags, hot, None, O.F32,
+                          out_dtype)
+        if split == -1:
+            assert np.array_equal(got.view(bits), ref.view(bits))
+        elif out_dtype == O.F16:
+            assert pooled_f16_close(got.view(np.uint16), ref.view(np.uint16))
+        else:
+            assert rel_close(got, ref, 1e-5)

@@ -107,6 +107,36 @@ def test_sanitize_default_row():
     lay.close()
 
 
+def test_out_of_range_keys_without_default_row():
+    """No default row: keys outside [0, rows) read nothing (the reference reads
+    past the table).  Their gathered rows keep the output's content; a bag
+    counts them as zero rows (the oracle on the table plus one zero row)."""
+    rng = np.random.default_rng(14)
+    rows, dim = 100, 16
+    tb = float_table(rng, rows, dim, O.F32)
+    keys = np.array([3, -1, 99, 100, 1 << 40, 42, -(1 << 40), 7], np.int64)
+    lay = GpuLayer(tb, _lib.DT_F32)
+    out = torch.full((keys.size, dim * 4), 0xAB, dtype=torch.uint8, device="cuda")
+    d_keys = to_dev(keys)
+    lay.lookup(d_keys, keys.size, out, dim * 4)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    inside = (keys >= 0) & (keys < rows)
+    assert np.array_equal(got[inside], tb[keys[inside]])
+    assert np.all(got[~inside] == 0xAB)
+    # pooled: 2 bags of 4, Sum and Mean
+    padded = np.concatenate([tb, np.zeros((1, tb.shape[1]), np.uint8)])
+    mapped = np.where(inside, keys, rows)
+    for pooling in (_lib.POOL_SUM, _lib.POOL_MEAN):
+        pout = torch.zeros((2, dim * 4), dtype=torch.uint8, device="cuda")
+        lay.pooled(d_keys, keys.size, pout, dim * 4, pooling, _lib.SPARSE_FIXED, None, 0, 4, None,
+                   _lib.DT_F32, _lib.DT_F32)
+        torch.cuda.synchronize()
+        ref = oracle_pool(padded, mapped, O.F32, dim, O.FIXED, pooling, None, 2, 4, None, O.F32, O.F32)
+        assert np.array_equal(pout.cpu().numpy().view(np.uint32).reshape(2, dim), ref.view(np.uint32))
+    lay.close()
+
+
 def test_invalid_arguments_raise_before_work():
     rng = np.random.default_rng(5)
     tb = float_table(rng, 16, 4, O.F32)
