@@ -288,6 +288,23 @@ __device__ __forceinline__ void decode(const Vec<VB>& v, const Meta& m,
 }
 
 // ---------------------------------------------------------------------------
+// shared pieces of the lookup kernels
+// ---------------------------------------------------------------------------
+// Readable zeros for keys that resolve to no row: their loads are pointed
+// here (offsets folded into the buffer) so that every load of a batch can be
+// issued unconditionally.  One copy per translation unit.
+constexpr int kZeroRowBytes = 4096;
+constexpr int64_t kZeroRowMask = kZeroRowBytes - 1;
+static __device__ __align__(16) uint8_t g_zero_row[kZeroRowBytes + 64] = {};
+
+// Adds the wave's per-lane miss counts to *counter (every lane active).
+__device__ __forceinline__ void add_misses(unsigned long long* counter, uint32_t n) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
+  if (__lane_id() == 0 && n) atomicAdd(counter, (unsigned long long)n);
+}
+
+// ---------------------------------------------------------------------------
 // key / row resolution
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t load_key(const void* keys, int key_bytes, int64_t i) {

@@ -1,0 +1,17 @@
+// pool_launch.hpp -- per-type-group launchers of the find-and-pool kernel
+// (pool_float.hip, pool_quant.hip, pool_ext.hip), called by launch_pool once
+// it has chosen the geometry.
+#pragma once
+
+#include "launch.hpp"
+
+namespace nve_amd {
+
+// kF32, kF16
+hipError_t launch_pool_float(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
+// kQI8F32, kQI8F16, kQU8F32, kQU8F16
+hipError_t launch_pool_quant(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
+// kXI8AF32, kXE4M3F32
+hipError_t launch_pool_ext(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
+
+}  // namespace nve_amd
