@@ -339,18 +339,25 @@ nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, c
   C_CATCH
 }
 
-nve_status_t nve_table_update(nve_table_t table, nve_context_t ctx, int64_t, const void*, int64_t,
-                              int64_t, const void*) {
+nve_status_t nve_table_update(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys,
+                              int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
-  return set_error(NVE_ERROR_NOT_IMPLEMENTED, "GPU table update is not part of this build");
+  C_TRY
+  table->ptr->update(*ctx->ptr, n, keys, value_stride, value_size, values);
+  return NVE_SUCCESS;
+  C_CATCH
 }
 
-nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, int64_t,
-                                         const void*, int64_t, int64_t, const void*,
-                                         nve_data_type_t) {
+nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, int64_t n,
+                                         const void* keys, int64_t value_stride,
+                                         int64_t value_size, const void* values,
+                                         nve_data_type_t value_type) {
   NEED_TABLE_CTX
-  return set_error(NVE_ERROR_NOT_IMPLEMENTED,
-                   "GPU table update_accumulate is not part of this build");
+  C_TRY
+  table->ptr->update_accumulate(*ctx->ptr, n, keys, value_stride, value_size, values,
+                                dtype_in(value_type));
+  return NVE_SUCCESS;
+  C_CATCH
 }
 
 nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {

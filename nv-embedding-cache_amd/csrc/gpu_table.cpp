@@ -103,7 +103,8 @@ void GpuTable::find(ExecutionContext& ctx, int64_t n, const void* keys, uint64_t
   }
 
   std::shared_lock<std::shared_mutex> lk(uvm_mu_, std::defer_lock);
-  if (uvm && !cfg_.private_stream) lk.lock();
+  // backing-table writers (update, accumulate, erase, clear) take it exclusively
+  if (uvm) lk.lock();
   GatherLaunch g{};
   g.keys = d_keys;
   g.key_bytes = key_bytes_;
@@ -140,7 +141,7 @@ void GpuTable::find_and_pool(ExecutionContext& ctx, int64_t n, const void* d_key
       is_rowwise(vdt) ? (cfg_.row_size_in_bytes - meta_bytes(vdt)) / value_elem_bytes(vdt)
                       : cfg_.row_size_in_bytes / std::max(1, dtype_size(vdt));
   std::shared_lock<std::shared_mutex> lk(uvm_mu_, std::defer_lock);
-  if (!cfg_.private_stream) lk.lock();
+  lk.lock();  // held off while the backing table is written
   if (pp.pooling_type == NVE_POOL_CONCATENATE) {
     GatherLaunch g{};
     g.keys = d_keys;

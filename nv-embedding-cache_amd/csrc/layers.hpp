@@ -94,6 +94,17 @@ class GPUEmbeddingLayer : public EmbeddingLayer {
   void lookup(ExecutionContext& ctx, int64_t num_keys, const void* keys, void* output,
               int64_t output_stride, uint64_t* hitmask, const PoolingParams* pp,
               float* hitrates) override;
+  // gpu_embedding_layer.cu:500-639: update / accumulate write the HBM table;
+  // insert, clear and erase have no effect on a linear table.
+  void insert(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+              int64_t value_size, const void* values, int64_t table_id) override;
+  void update(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+              int64_t value_size, const void* values, int64_t table_id) override;
+  void accumulate(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+                  int64_t value_size, const void* values, int value_type,
+                  int64_t table_id) override;
+  void clear(ExecutionContext& ctx) override;
+  void erase(ExecutionContext& ctx, int64_t n, const void* keys, int64_t table_id) override;
   const GPUEmbeddingLayerConfig& config() const { return cfg_; }
 
  private:
@@ -143,6 +154,14 @@ class GpuTable {
   void insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* keys);  // gpu_table.cu:494-576
   void erase(ExecutionContext& ctx, int64_t n, const void* keys);
   void clear(ExecutionContext& ctx);
+  // gpu_table.cu:579-681 / :683-1046: resident keys' cache rows are
+  // overwritten (update) or added to (update_accumulate, f32/f16 of the
+  // table's type); the backing table gets the same change unless
+  // disable_uvm_update is set.
+  void update(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+              int64_t value_size, const void* values);
+  void update_accumulate(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+                         int64_t value_size, const void* values, int update_dtype);
 
   // GpuTable::find_and_pool (gpu_table.cu:1049-1104), keys already on the device.
   void find_and_pool(ExecutionContext& ctx, int64_t n, const void* d_keys, const PoolingParams& pp,
@@ -161,6 +180,9 @@ class GpuTable {
   // runs on stream s (the modify stream or the table's private stream)
   void modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
                      const uint8_t* rows, int64_t row_stride, bool from_uvm);
+  // cache rows of resident keys: invalidate -> drain -> copy or add -> commit
+  void modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
+                   const uint8_t* d_vals, int64_t value_stride, bool accumulate, int dtype);
   void build_decay_table();
   int key_bytes_;
   GPUTableConfig cfg_;
@@ -225,6 +247,11 @@ class LinearUVMEmbeddingLayer : public EmbeddingLayer {
               float* hitrates) override;
   void insert(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
               int64_t value_size, const void* values, int64_t table_id) override;
+  void update(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+              int64_t value_size, const void* values, int64_t table_id) override;
+  void accumulate(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
+                  int64_t value_size, const void* values, int value_type,
+                  int64_t table_id) override;
   void clear(ExecutionContext& ctx) override;
   void erase(ExecutionContext& ctx, int64_t n, const void* keys, int64_t table_id) override;
 

@@ -3,6 +3,7 @@
 
 #include "kernels/cache_launch.hpp"
 
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 
@@ -247,6 +248,49 @@ const void* device_input(ExecutionContext& ctx, const char* name, const void* p,
   void* d = ctx.buffer(name, bytes, false);
   NVE_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream));
   return d;
+}
+
+const void* host_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
+                       hipStream_t stream) {
+  if (p == nullptr || bytes == 0) return p;
+  if (mem_kind(p) != MemKind::Device) return p;
+  void* h = ctx.buffer(name, bytes, true);
+  NVE_HIP(hipMemcpyAsync(h, p, bytes, hipMemcpyDeviceToHost, stream));
+  NVE_HIP(hipStreamSynchronize(stream));
+  return h;
+}
+
+float half_bits_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  if (e == 0) {
+    const float f = std::ldexp((float)m, -24);  // zero or subnormal: m * 2^-24, exact
+    return sign ? -f : f;
+  }
+  const uint32_t bits = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t float_to_half_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // >= 65520 rounds to infinity
+  if (ax < 0x38800000u) {
+    // below 2^-14: a multiple of 2^-24 after rounding; scaling by 2^24 is exact
+    float v;
+    std::memcpy(&v, &ax, 4);
+    return (uint16_t)(sign | (uint16_t)std::nearbyint(v * 16777216.0f));
+  }
+  uint32_t h = ((((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // a carry bumps the exponent correctly
+  return (uint16_t)(sign | h);
 }
 
 void* device_output(ExecutionContext& ctx, const char* name, void* p, size_t bytes) {

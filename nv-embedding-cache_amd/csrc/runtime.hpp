@@ -172,6 +172,15 @@ MemKind mem_kind(const void* p);
 const void* device_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
                          hipStream_t stream);
 
+// Host-readable view of `bytes` at `p`: p itself unless it is device memory,
+// else a synchronous copy (on `stream`) into the context's host buffer `name`.
+const void* host_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
+                       hipStream_t stream);
+
+// fp16 <-> fp32 on the host (round to nearest even; NaN stays NaN).
+float half_bits_to_float(uint16_t h);
+uint16_t float_to_half_bits(float f);
+
 // Device-writable target for `bytes` at `p`; when it differs from p, call
 // finish_output afterwards to copy it back.
 void* device_output(ExecutionContext& ctx, const char* name, void* p, size_t bytes);

@@ -2,8 +2,8 @@
 (python/pynve/torch/nve_tensors.py:18-80).
 
 It wraps the table's storage and keeps a reference to the layer binding
-(`emb_layer`).  Only lookups are in this build, so `add_` -- the optimizer's
-update hook in the reference, which accumulates into the caches -- raises.
+(`emb_layer`).  `add_` is the optimizer's update hook: a sparse row-gradient
+is accumulated into the layer's table and caches (nve_tensors.py:64-80).
 """
 import torch
 
@@ -26,6 +26,15 @@ class CachedTable(torch.nn.parameter.Parameter):
         return state
 
     def add_(self, other, *, alpha=1):
-        raise _lib.NotImplementedInBuild(
-            _lib.NOT_IMPLEMENTED, "Optimizer updates of an NVEmbedding table (accumulate) "
-            "are not part of this build")
+        """self += alpha * other for a sparse `other` over rows (its nonzero
+        rows go to the layer's accumulate, which updates the table and every
+        cache that holds them)."""
+        if not other.is_sparse:
+            raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, "add_ takes a sparse row tensor")
+        factored = (other * alpha).coalesce()
+        keys = factored.indices()[0].contiguous()
+        values = factored.values().to(self.dtype).contiguous()
+        stream = torch.cuda.current_stream().cuda_stream
+        self.emb_layer.accumulate(factored._nnz(), keys.data_ptr(), values.data_ptr(), stream)
+        torch.cuda.current_stream().synchronize()  # keys / values are temporaries
+        return self

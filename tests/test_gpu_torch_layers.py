@@ -225,8 +225,29 @@ def test_backward_is_not_in_this_build():
         out.sum().backward()
     infer = make(LT.GPULayer, w, train=False)
     assert torch.equal(infer(keys), w[keys.cpu()].cuda())
-    with pytest.raises(NotImplementedError):
-        train.update(keys, torch.zeros(3, 4, device="cuda"))
+
+
+@pytest.mark.parametrize("layer_type", [LT.GPULayer, LT.LinearUVM], ids=["gpu", "uvm"])
+def test_layer_update_and_sparse_add(layer_type):
+    # NVEmbeddingBase.update (nve_layers.py:356-367) and CachedTable.add_ (nve_tensors.py:64-80):
+    # rows change in the table and in the GPU cache; dyadic values keep the sums exact
+    rng = np.random.default_rng(9)
+    rows, dim = 2000, 16
+    w = torch.from_numpy((rng.integers(-8, 9, size=(rows, dim)) / 64.0).astype(np.float32))
+    layer = make(layer_type, w, cache=1 << 20)
+    keys = torch.tensor([3, 17, 1999, 256], dtype=torch.int64, device="cuda")
+    with torch.no_grad():
+        layer(keys)  # (UVM: the lookup may start caching these rows)
+        new = torch.full((4, dim), 0.5, device="cuda")
+        layer.update(keys, new)
+        torch.cuda.synchronize()
+        assert torch.equal(layer(keys), new)
+        grad = torch.sparse_coo_tensor(torch.tensor([[3, 3, 5]]), torch.full((3, dim), 0.25),
+                                       (rows, dim)).cuda()
+        layer.weight.add_(grad, alpha=-1.0)
+        out = layer(torch.tensor([3, 5, 17], dtype=torch.int64, device="cuda"))
+        exp = torch.stack([new[0] - 0.5, w[5].cuda() - 0.25, new[1]])
+        assert torch.equal(out, exp)
 
 
 def test_direct_binding_calls():
