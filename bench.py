@@ -272,7 +272,6 @@ def run_workload(args, torch, _lib):
             assert hip.hipMemcpy(host_ptr.value + r0 * width, tmp.data_ptr(), (r1 - r0) * width, 2) == 0
         del tmp
         torch.cuda.synchronize()
-
         class _Host:  # the table's address, as the layer config wants it
             def data_ptr(self):
                 return host_ptr.value
@@ -289,6 +288,10 @@ def run_workload(args, torch, _lib):
         tc.value_dtype = _lib.DT_F16
         tc.uvm_table = host.data_ptr()
         tc.uvm_num_rows = rows
+        tc.kernel_mode_type = args.kernel_mode
+        pipe_params = (ctypes.c_uint64 * 2)(1024, 16)  # PipelineGather {task_size, num_aux_streams}
+        if args.kernel_mode == 3:
+            tc.kernel_mode_value = ctypes.addressof(pipe_params)
         table = ctypes.c_void_p()
         _lib.call("nve_gpu_table_create", ctypes.byref(table), _lib.KEY_INT64, ctypes.byref(tc), None)
         lc = L.nve_linear_uvm_layer_config_default()
@@ -296,15 +299,20 @@ def run_workload(args, torch, _lib):
         layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
         _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), table, None)
         _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
-        out = torch.empty((bags, dim), dtype=torch.float16, device="cuda")
+        concat = args.c3_concat
+        out = torch.empty((nkeys if concat else bags, dim), dtype=torch.float16, device="cuda")
         hr = (ctypes.c_float * 1)()
         kp = [ctypes.c_void_p(b.data_ptr()) for b in batches]
         rates = []
 
         def lookup(i):
-            _lib.check(L.nve_layer_lookup_pooled(layer, ctx, nkeys, kp[i], ctypes.c_void_p(out.data_ptr()),
-                                                 width, None, _lib.POOL_SUM, _lib.SPARSE_FIXED, None, 0, hot,
-                                                 None, 0, _lib.DT_F16, hr))
+            if concat:  # one row per key (NVEmbedding forward; the reference bench's shape)
+                _lib.check(L.nve_layer_lookup(layer, ctx, nkeys, kp[i], ctypes.c_void_p(out.data_ptr()), width,
+                                              None, hr))
+            else:
+                _lib.check(L.nve_layer_lookup_pooled(layer, ctx, nkeys, kp[i], ctypes.c_void_p(out.data_ptr()),
+                                                     width, None, _lib.POOL_SUM, _lib.SPARSE_FIXED, None, 0,
+                                                     hot, None, 0, _lib.DT_F16, hr))
             _lib.call("nve_context_wait", ctx)  # joins an auto-insert launched by this lookup
             rates.append(hr[0])
 
@@ -330,16 +338,20 @@ def run_workload(args, torch, _lib):
         log(f"c3: {ms * 1000:.1f} us/step (events), {wall * 1000:.1f} us/step (wall), mean hit rate {hit:.4f}")
         ms = max(ms, wall)  # the step includes a host sync (hit rate) and any insert
         # HBM: keys + 8 tags (64 B) per key + cached rows; host link: missed rows
-        alg = nkeys * (8 + 64) + int(nkeys * hit) * width + int(nkeys * (1 - hit)) * width + bags * width
+        alg = (nkeys * (8 + 64) + int(nkeys * hit) * width + int(nkeys * (1 - hit)) * width
+               + (nkeys if concat else bags) * width)
         cfg_out.update({"host_table_rows": rows, "cache_gib": args.c3_cache_gib, "keys_per_batch": nkeys,
-                        "zipf_alpha": alpha, "bags": bags, "hotness": hot, "mean_hit_rate": round(hit, 4),
+                        "zipf_alpha": alpha, "mean_hit_rate": round(hit, 4),
                         "host_link_bytes_per_step": int(nkeys * (1 - hit)) * width,
-                        "step": "lookup_pooled + hit-rate readback + auto-insert when the heuristic fires"})
+                        "lookup": "concat" if concat else f"pooled {bags} x {hot} Sum",
+                        "kernel_mode": args.kernel_mode,
+                        "step": "lookup + hit-rate readback + auto-insert when the heuristic fires"})
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
         _lib.call("nve_table_destroy", table)
         hip.hipHostFree(host_ptr)
-        kernel = "pool_kernel (cache + host misses)"
+        kernel = ("gather_kernel / SortGather / PipelineGather (cache + host misses)" if concat
+                  else "pool_kernel (cache + host misses)")
     elif w == "c5":
         T, B, dim = 26, 8192, 128
         cg = torch.Generator()
@@ -421,6 +433,9 @@ def main():
     # table:cache ratio at 256M rows (65.5 GB) and a 20 GiB cache
     ap.add_argument("--c3-rows", type=int, default=256_000_000, help="c3: host table rows")
     ap.add_argument("--c3-cache-gib", type=int, default=20, help="c3: GPU cache size in GiB")
+    ap.add_argument("--c3-concat", action="store_true", help="c3: one row per key instead of pooled bags")
+    ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],
+                    help="c3: GPU table lookup mode (0 auto, 1 LookupUVM, 2 SortGather, 3 PipelineGather)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",

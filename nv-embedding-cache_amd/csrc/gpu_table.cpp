@@ -27,6 +27,13 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   NVE_CHECK(cfg_.uvm_table == nullptr || cfg_.uvm_num_rows > 0,
             "uvm_num_rows must be set to the number of rows in uvm_table");
   NVE_CHECK(cfg_.max_modify_size > 0, "max_modify_size must be positive");
+  NVE_CHECK_ARG(cfg_.kernel_mode_type <= 3, "Unsupported kernel_mode_type ", cfg_.kernel_mode_type);
+  if (cfg_.kernel_mode_type == 3 && cfg_.kernel_mode_value != 0) {
+    // PipelineGather: kernel_mode_value points at {task_size, num_aux_streams}
+    // (GatherKernelPipelineParams, pipeline_gather.cuh:33-36), read once here
+    const uint64_t* params = reinterpret_cast<const uint64_t*>(cfg_.kernel_mode_value);
+    if (params[0] > 0) pipeline_task_size_ = params[0];
+  }
   if (is_rowwise(cfg_.value_dtype))
     NVE_CHECK(cfg_.row_size_in_bytes % 2 == 0, "Quantized rows must have an even width");
   const uint64_t per_set = align16((uint64_t)key_bytes * kWays) +
@@ -67,6 +74,7 @@ GpuTable::~GpuTable() {
 RowSource GpuTable::row_source(bool with_uvm) const {
   RowSource s{};
   s.table = with_uvm ? static_cast<const uint8_t*>(cfg_.uvm_table) : nullptr;
+  s.num_rows = with_uvm ? (uint64_t)cfg_.uvm_num_rows : 0;  // misses outside it read nothing
   s.row_bytes = (uint64_t)cfg_.row_size_in_bytes;
   s.load_indices = 1;
   s.cache_data = data_;
@@ -122,7 +130,15 @@ void GpuTable::find(ExecutionContext& ctx, int64_t n, const void* keys, uint64_t
     g.out = ctx.buffer("find_scratch", (size_t)n * cfg_.row_size_in_bytes);
     g.out_stride = cfg_.row_size_in_bytes;
   }
-  NVE_HIP(launch_gather(g, stream));
+  if (uvm && d_vals != nullptr) {
+    switch (uvm_mode(n)) {
+      case UvmMode::Lookup: NVE_HIP(launch_gather(g, stream)); break;
+      case UvmMode::SortGather: find_sort_gather(ctx, g, stream); break;
+      case UvmMode::PipelineGather: find_pipeline_gather(ctx, g, stream); break;
+    }
+  } else {
+    NVE_HIP(launch_gather(g, stream));
+  }
   if (d_mask && d_mask != hit_mask)
     NVE_HIP(hipMemcpyAsync(hit_mask, d_mask, mask_bytes, hipMemcpyDeviceToHost, stream));
   if (values) finish_output(values, d_vals, out_bytes, stream);

@@ -381,7 +381,9 @@ __device__ __forceinline__ uint64_t resolve_row(const RowSource& src, int key_by
     return (uint64_t)src.cache_data + ((uint64_t)set * 8 + way) * src.row_bytes;
   }
   *miss = true;
-  return src.table ? (uint64_t)src.table + (uint64_t)key * src.row_bytes : 0;
+  // the backing row; none for a table without one, or a key outside it
+  if (src.table == nullptr || (src.num_rows != 0 && (uint64_t)key >= src.num_rows)) return 0;
+  return (uint64_t)src.table + (uint64_t)key * src.row_bytes;
 }
 
 }  // namespace nve_amd

@@ -21,7 +21,7 @@ struct RowSource {
   const uint8_t* cache_data; // null: no cache
   const void* cache_tags;    // num_sets*8 tags of the key type
   uint64_t num_sets;
-  uint64_t num_rows;         // linear table only: keys >= num_rows stay unresolved (0 = no bound)
+  uint64_t num_rows;         // rows of `table`: keys >= num_rows read nothing (0 = no bound)
 };
 
 // One output row per key: the raw stored row (raw != 0) or its dequantized

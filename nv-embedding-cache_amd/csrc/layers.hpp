@@ -180,6 +180,13 @@ class GpuTable {
   // runs on stream s (the modify stream or the table's private stream)
   void modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
                      const uint8_t* rows, int64_t row_stride, bool from_uvm);
+  // lookup modes over the backing table (gpu_table.cu:271-287): the direct
+  // lookup, SortGather (misses and hits sorted apart) and PipelineGather
+  // (host threads copy the missed rows); all write the same output
+  enum class UvmMode { Lookup, SortGather, PipelineGather };
+  UvmMode uvm_mode(int64_t n) const;
+  void find_sort_gather(ExecutionContext& ctx, const GatherLaunch& g, hipStream_t s);
+  void find_pipeline_gather(ExecutionContext& ctx, const GatherLaunch& g, hipStream_t s);
   // cache rows of resident keys: invalidate -> drain -> copy or add -> commit
   void modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
                    const uint8_t* d_vals, int64_t value_stride, bool accumulate, int dtype);
@@ -195,6 +202,7 @@ class GpuTable {
   float decay_rate_ = 0.95f;  // EmbedCacheSA::CacheConfig default (ec_set_associative.h:120)
   float* decay_table_ = nullptr;
   int64_t decay_len_ = 0;
+  uint64_t pipeline_task_size_ = 1024;  // PipelineGather keys per host task
   std::mutex modify_mu_;        // one modify at a time
   std::shared_mutex uvm_mu_;    // lookups shared, modifies exclusive
 };

@@ -126,7 +126,28 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
   NVE_HIP(hipMemcpyAsync(collected_.data() + (size_t)collected_n_ * key_bytes_, d_keys,
                          (size_t)part * key_bytes_, hipMemcpyDefault, ctx.lookup_stream()));
   NVE_HIP(hipStreamSynchronize(ctx.lookup_stream()));
-  collected_n_ += part;
+  // keys outside the backing table (no default row configured) cannot be
+  // inserted from it: drop them here
+  {
+    const uint64_t rows = (uint64_t)table_->config().uvm_num_rows;
+    uint8_t* base = collected_.data() + (size_t)collected_n_ * key_bytes_;
+    int64_t kept = 0;
+    for (int64_t i = 0; i < part; ++i) {
+      int64_t k;
+      if (key_bytes_ == 4) {
+        int32_t k32;
+        std::memcpy(&k32, base + (size_t)i * 4, 4);
+        k = k32;
+      } else {
+        std::memcpy(&k, base + (size_t)i * 8, 8);
+      }
+      if ((uint64_t)k >= rows) continue;
+      if (kept != i) std::memmove(base + (size_t)kept * key_bytes_, base + (size_t)i * key_bytes_, key_bytes_);
+      ++kept;
+    }
+    collected_n_ += kept;
+    collected_.resize((size_t)collected_n_ * key_bytes_);
+  }
   if (collected_n_ < min_size) return;
   std::vector<uint8_t> keys;
   keys.swap(collected_);

@@ -404,11 +404,18 @@ class LinearUVMEmbedding(NVEmbedBinding):
             cfg.private_stream = self._private_stream.cuda_stream
         cfg.uvm_table = mem_block.get_ptr()
         cfg.uvm_num_rows = self.num_embeddings_
-        # kernel modes (binding_layers.hpp:565-576) are recorded; one fused
-        # hit/miss kernel serves all of them in this build
+        # lookup modes (binding_layers.hpp:565-576; KernelType, gpu_table.hpp:37-42):
+        # 0 direct below 2^20 keys else SortGather, 1 direct, 2 SortGather
+        # (value: tile size), 3 PipelineGather (value: pointer to
+        # {task_size, num_aux_streams}, read when the table is created)
         cfg.kernel_mode_type = int(config.kernel_mode)
-        if config.kernel_mode == 1:  # SortGather: minimum key count
+        if config.kernel_mode == 2:
             cfg.kernel_mode_value = int(config.kernel_mode_value_1) if config.kernel_mode_value_1 > 0 else 1024
+        elif config.kernel_mode == 3:
+            self._pipeline_params = (ctypes.c_uint64 * 2)(
+                int(config.kernel_mode_value_1) if config.kernel_mode_value_1 > 0 else 1024,
+                int(config.kernel_mode_value_2) if config.kernel_mode_value_2 > 0 else 16)
+            cfg.kernel_mode_value = ctypes.addressof(self._pipeline_params)
         t = ctypes.c_void_p()
         _lib.call("nve_gpu_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(cfg), None)
         self._table = t.value

@@ -24,7 +24,8 @@ class CachedTable:
     """GPU table (+ optional pinned backing table) whose cache state is copied
     from an oracle cache model."""
 
-    def __init__(self, uvm_bytes, cache_bytes, key_bytes=8, with_uvm=True, value_dtype=_lib.DT_F32):
+    def __init__(self, uvm_bytes, cache_bytes, key_bytes=8, with_uvm=True, value_dtype=_lib.DT_F32,
+                 kernel_mode_type=0, kernel_mode_value=0):
         self.rows, self.width = uvm_bytes.shape
         self.key_bytes = key_bytes
         self.uvm_np = np.ascontiguousarray(uvm_bytes)
@@ -34,6 +35,8 @@ class CachedTable:
         cfg.cache_size = cache_bytes
         cfg.row_size_in_bytes = self.width
         cfg.value_dtype = value_dtype
+        cfg.kernel_mode_type = kernel_mode_type
+        cfg.kernel_mode_value = kernel_mode_value
         if with_uvm:
             cfg.uvm_table = self.h_uvm.data_ptr()
             cfg.uvm_num_rows = self.rows

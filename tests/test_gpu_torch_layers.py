@@ -100,6 +100,22 @@ def test_random_bags_against_oracle(layer_type, dtype, mode, weighted):
                 assert pooled_f16_close(out.view(np.uint16), ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("kernel_mode", [1, 2, 3])
+def test_linear_gather_flows(kernel_mode):
+    # test_pytorch.py:367-384: every lookup mode of a LinearUVM layer returns torch.nn.Embedding's rows
+    torch.manual_seed(10)
+    ref = torch.nn.Embedding(200000, 4, device="cuda")
+    layer = make(LT.LinearUVM, ref.weight.detach(), cache=1 << 20,
+                 config={"kernel_mode": kernel_mode, "kernel_mode_value_1": 256})
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(kernel_mode)
+    with torch.no_grad():
+        for _ in range(5):
+            keys = torch.randint(0, 200000, (20000,), generator=gen, device="cuda")
+            keys[:5000] = keys[:5000] % 3000
+            assert torch.equal(layer(keys), ref(keys))
+
+
 def test_multi_stream():
     # test_pytorch.py:554-576
     torch.manual_seed(2)

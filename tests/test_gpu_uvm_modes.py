@@ -1,0 +1,94 @@
+"""GPU parity of the lookup modes over a host-resident backing table
+(get_kernel_mode, gpu_table.cu:271-287): LookupUVM, SortGather
+(ec_set_associative.cuh:966-1057) and PipelineGather (pipeline_gather.cuh:203-412)
+write the same rows -- each key's cache row on a hit, its backing row on a
+miss, nothing for a key outside the table -- and count the same misses.
+Checked against the oracle's cache model and across modes, bytewise."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from nve_helpers import float_table, stream_ptr, to_dev, vp
+from oracle import oracle as O
+from pynve import _lib
+from test_gpu_cache_lookup import CachedTable, warm
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+LOOKUP, SORT, PIPE = 1, 2, 3
+
+
+def run_find(ct, keys, dim4, fill=0x5A):
+    out = torch.full((keys.size, dim4), fill, dtype=torch.uint8, device="cuda")
+    d_keys = to_dev(keys)
+    _lib.call("nve_table_reset_lookup_counter", ct.table, ct.ctx)
+    _lib.call("nve_table_find", ct.table, ct.ctx, keys.size, vp(d_keys), None, dim4, vp(out), None)
+    cnt = ctypes.c_int64()
+    _lib.call("nve_table_get_lookup_counter", ct.table, ct.ctx, ctypes.byref(cnt))
+    return out.cpu().numpy(), cnt.value
+
+
+def expected(ct, keys, dim4, fill=0x5A):
+    """Cache slot on a hit, backing row on a miss, untouched for a key outside
+    the table (the model resolves it to an address past the table)."""
+    rows_ptr, hits, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    data = ct.model.data().reshape(-1)
+    base_d, base_u = data.ctypes.data, ct.uvm_np.ctypes.data
+    exp = np.full((keys.size, dim4), fill, np.uint8)
+    for i in range(keys.size):
+        p = int(rows_ptr[i])
+        if base_d <= p < base_d + data.nbytes:
+            exp[i] = data[p - base_d:p - base_d + dim4]
+        elif 0 <= int(keys[i]) < ct.rows:
+            exp[i] = ct.uvm_np.reshape(-1)[p - base_u:p - base_u + dim4]
+    return exp, misses
+
+
+@pytest.mark.parametrize("key_bytes", [8, 4])
+@pytest.mark.parametrize("n", [3000, 70000])
+def test_modes_write_the_same_rows(key_bytes, n):
+    rng = np.random.default_rng(60 + n + key_bytes)
+    rows, dim = 50000, 32
+    uvm = float_table(rng, rows, dim, O.F32, dyadic_values=False)
+    kdt = np.int64 if key_bytes == 8 else np.int32
+    keys = rng.integers(0, rows, size=n).astype(kdt)
+    keys[: n // 3] = rng.integers(0, 4000, size=n // 3)  # mostly cached
+    keys[rng.random(n) < 0.01] = rows + 5                # outside the table
+    keys[rng.random(n) < 0.01] = -3
+    params = (ctypes.c_uint64 * 2)(97, 4)  # PipelineGather: 97 keys per host task
+    outs = {}
+    for mode, value in ((LOOKUP, 0), (SORT, 0), (PIPE, ctypes.addressof(params)), (0, 1000)):
+        ct = CachedTable(uvm, 512 * 1024, key_bytes, kernel_mode_type=mode, kernel_mode_value=value)
+        rng2 = np.random.default_rng(7)
+        warm(ct, rng2, 6000, np.arange(0, 4000))
+        got, misses = run_find(ct, keys, dim * 4)
+        exp, exp_misses = expected(ct, keys, dim * 4)
+        assert np.array_equal(got, exp), f"mode {mode}"
+        assert misses == exp_misses, f"mode {mode}"
+        outs[mode] = got
+        ct.close()
+    assert all(np.array_equal(outs[LOOKUP], o) for o in outs.values())
+
+
+def test_pipeline_default_params_and_all_misses():
+    rng = np.random.default_rng(61)
+    rows, dim = 20000, 64
+    uvm = float_table(rng, rows, dim, O.F16, dyadic_values=False)
+    ct = CachedTable(uvm, 256 * 1024, 8, value_dtype=_lib.DT_F16, kernel_mode_type=PIPE)
+    keys = rng.integers(0, rows, size=5000).astype(np.int64)  # empty cache: every key misses
+    got, misses = run_find(ct, keys, dim * 2)
+    assert misses == keys.size
+    assert np.array_equal(got, uvm[keys])
+    ct.close()
+
+
+def test_unknown_kernel_mode_is_rejected():
+    L = _lib.load()
+    cfg = L.nve_gpu_table_config_default()
+    cfg.cache_size, cfg.row_size_in_bytes, cfg.value_dtype = 1 << 20, 64, _lib.DT_F32
+    cfg.kernel_mode_type = 7
+    t = ctypes.c_void_p()
+    with pytest.raises(_lib.InvalidArgument, match="kernel_mode_type"):
+        _lib.call("nve_gpu_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(cfg), None)
