@@ -105,6 +105,15 @@ NVE_C_API nve_status_t nve_amd_gpu_table_import_state(nve_table_t table, const v
 /* Device address of the cache rows ((set*8 + way) * row_size_in_bytes). */
 NVE_C_API nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out);
 
+/* GpuTable::insert_from_uvm (include/gpu_table.hpp:160-167, gpu_table.cu:494-576):
+ * insert keys whose rows are read from the table's backing (UVM) table at
+ * uvm_table + key * row_size_in_bytes.  The reference's C ABI reaches it only
+ * through a LinearUVM layer's auto-insert; this entry exposes it directly.
+ * Keys may live in host or device memory; keys outside [0, uvm_num_rows) are
+ * not inserted. */
+NVE_C_API nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx,
+                                                     int64_t n, const void* keys);
+
 #ifdef __cplusplus
 }
 #endif

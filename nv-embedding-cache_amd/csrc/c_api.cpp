@@ -869,6 +869,15 @@ nve_status_t nve_amd_gpu_table_import_state(nve_table_t table, const void* tags,
   C_CATCH
 }
 
+nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx, int64_t n,
+                                           const void* keys) {
+  NEED_TABLE_CTX
+  C_TRY
+  table->ptr->insert_from_uvm(*ctx->ptr, n, keys);
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
 nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out) {
   if (!table || !table->ptr || !out)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");

@@ -5,8 +5,11 @@
 // :667-685): per set 8 tags of the key type, 8 rows, 8 float counters and one
 // int64 timestamp.  num_sets = cache_size / (align16(8*sizeof(Key)) +
 // align16(8*row) + align16(8*4)), the device-modify counter bytes included in
-// the per-set size (ec_set_associative_device_modify.cuh:472-474).  Rows live
-// set-major at data + (set*8 + way)*row so one set's 8 rows are contiguous.
+// the per-set size (ec_set_associative_device_modify.cuh:472-474).  With
+// modify_on_gpu = false (CacheSAHostModify) the counters and timestamps live
+// in host memory and the per-set size has no counter term
+// (ec_set_associative_host_modify.h:519-534).  Rows live set-major at
+// data + (set*8 + way)*row so one set's 8 rows are contiguous.
 #include <algorithm>
 #include <climits>
 #include <cstring>
@@ -38,7 +41,7 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
     NVE_CHECK(cfg_.row_size_in_bytes % 2 == 0, "Quantized rows must have an even width");
   const uint64_t per_set = align16((uint64_t)key_bytes * kWays) +
                            align16((uint64_t)cfg_.row_size_in_bytes * kWays) +
-                           align16(sizeof(float) * kWays);
+                           (cfg_.modify_on_gpu ? align16(sizeof(float) * kWays) : 0);
   num_sets_ = cfg_.cache_size / per_set;
   NVE_CHECK(num_sets_ > 0, "Memory allocated to the cache is too small");
   NVE_CHECK(num_sets_ <= UINT32_MAX, "Too many cache sets");
@@ -49,13 +52,20 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   else
     NVE_HIP(hipMalloc((void**)&data_, data_bytes));
   NVE_HIP(hipMalloc(&tags_, (size_t)ways * key_bytes));
-  NVE_HIP(hipMalloc((void**)&counters_, (size_t)ways * sizeof(float)));
-  NVE_HIP(hipMalloc((void**)&set_ts_, (size_t)num_sets_ * sizeof(int64_t)));
   NVE_HIP(launch_fill_tags(tags_, (int64_t)ways, key_bytes, cfg_.invalid_key, nullptr));
-  NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), (int64_t)ways, 0, nullptr));
-  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, nullptr));
+  if (cfg_.modify_on_gpu) {
+    NVE_HIP(hipMalloc((void**)&counters_, (size_t)ways * sizeof(float)));
+    NVE_HIP(hipMalloc((void**)&set_ts_, (size_t)num_sets_ * sizeof(int64_t)));
+    NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), (int64_t)ways, 0, nullptr));
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, nullptr));
+    build_decay_table();
+  } else {
+    h_tags_.resize((size_t)ways * key_bytes);
+    for (uint64_t w = 0; w < ways; ++w) set_h_tag(w, cfg_.invalid_key);
+    h_counters_.assign((size_t)ways, 0.0f);
+    h_set_ts_.assign((size_t)num_sets_, 0);
+  }
   NVE_HIP(hipDeviceSynchronize());
-  build_decay_table();
 }
 
 GpuTable::~GpuTable() {
@@ -208,11 +218,40 @@ void GpuTable::erase(ExecutionContext& ctx, int64_t n, const void* keys) {
   std::unique_lock<std::shared_mutex> lk(uvm_mu_);
   StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
   const hipStream_t stream = q.stream;
+  if (!cfg_.modify_on_gpu) {
+    // CacheSAHostModify::invalidate (ec_set_associative_host_modify.h:134-178):
+    // every matching way of the host tags is emptied (its counter stays) and
+    // the device tags follow
+    const uint8_t* hk = static_cast<const uint8_t*>(
+        host_input(ctx, "modify_keys_host", keys, (size_t)n * key_bytes_, stream));
+    std::vector<uint64_t> slot;
+    std::vector<int64_t> tag;
+    std::vector<uint64_t> src;
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t k = load_key(hk, i);
+      const uint64_t set = set_of(k);
+      for (int w = 0; w < kWays; ++w) {
+        const uint64_t sl = set * kWays + (uint64_t)w;
+        if (key_of(h_tag(sl), set) == k) {
+          set_h_tag(sl, cfg_.invalid_key);
+          slot.push_back(sl);
+          tag.push_back(cfg_.invalid_key);
+          src.push_back(0);
+        }
+      }
+    }
+    apply_records(ctx, stream, slot, tag, src, true);
+    return;
+  }
   const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, stream);
   NVE_HIP(launch_cache_erase(tags_, d_keys, n, key_bytes_, num_sets_, cfg_.invalid_key, stream));
   NVE_HIP(hipStreamSynchronize(stream));
 }
 
+// clear_cache: all ways empty, the insert clock and the set timestamps back to
+// 0 (ec_set_associative_device_modify.cuh:205-222); the host-policy cache also
+// zeroes its counters (ec_set_associative_host_modify.h:192-211).  The device
+// policy leaves the counters: an empty way counts as 0 there whatever it holds.
 void GpuTable::clear(ExecutionContext& ctx) {
   ScopedDevice sd(cfg_.device_id);
   std::lock_guard<std::mutex> mk(modify_mu_);
@@ -221,8 +260,14 @@ void GpuTable::clear(ExecutionContext& ctx) {
   const hipStream_t stream = q.stream;
   const int64_t ways = (int64_t)num_sets_ * kWays;
   NVE_HIP(launch_fill_tags(tags_, ways, key_bytes_, cfg_.invalid_key, stream));
-  NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), ways, 0, stream));
-  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, stream));
+  if (cfg_.modify_on_gpu) {
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, stream));
+  } else {
+    for (int64_t w = 0; w < ways; ++w) set_h_tag((uint64_t)w, cfg_.invalid_key);
+    std::fill(h_counters_.begin(), h_counters_.end(), 0.0f);
+    std::fill(h_set_ts_.begin(), h_set_ts_.end(), 0);
+  }
+  global_ts_ = 0;
   NVE_HIP(hipStreamSynchronize(stream));
 }
 
@@ -232,8 +277,13 @@ void GpuTable::export_state(void* tags, float* counters, int64_t* set_ts, int64_
   NVE_HIP(hipDeviceSynchronize());
   const size_t ways = (size_t)num_sets_ * kWays;
   if (tags) NVE_HIP(hipMemcpy(tags, tags_, ways * key_bytes_, hipMemcpyDefault));
-  if (counters) NVE_HIP(hipMemcpy(counters, counters_, ways * sizeof(float), hipMemcpyDefault));
-  if (set_ts) NVE_HIP(hipMemcpy(set_ts, set_ts_, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+  if (cfg_.modify_on_gpu) {
+    if (counters) NVE_HIP(hipMemcpy(counters, counters_, ways * sizeof(float), hipMemcpyDefault));
+    if (set_ts) NVE_HIP(hipMemcpy(set_ts, set_ts_, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+  } else {
+    if (counters) std::memcpy(counters, h_counters_.data(), ways * sizeof(float));
+    if (set_ts) std::memcpy(set_ts, h_set_ts_.data(), num_sets_ * sizeof(int64_t));
+  }
   if (global_ts) *global_ts = global_ts_;
 }
 
@@ -245,8 +295,14 @@ void GpuTable::import_state(const void* tags, const float* counters, const int64
   NVE_HIP(hipDeviceSynchronize());
   const size_t ways = (size_t)num_sets_ * kWays;
   if (tags) NVE_HIP(hipMemcpy(tags_, tags, ways * key_bytes_, hipMemcpyDefault));
-  if (counters) NVE_HIP(hipMemcpy(counters_, counters, ways * sizeof(float), hipMemcpyDefault));
-  if (set_ts) NVE_HIP(hipMemcpy(set_ts_, set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+  if (cfg_.modify_on_gpu) {
+    if (counters) NVE_HIP(hipMemcpy(counters_, counters, ways * sizeof(float), hipMemcpyDefault));
+    if (set_ts) NVE_HIP(hipMemcpy(set_ts_, set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+  } else {
+    if (tags) NVE_HIP(hipMemcpy(h_tags_.data(), tags, ways * key_bytes_, hipMemcpyDefault));
+    if (counters) NVE_HIP(hipMemcpy(h_counters_.data(), counters, ways * sizeof(float), hipMemcpyDefault));
+    if (set_ts) NVE_HIP(hipMemcpy(h_set_ts_.data(), set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+  }
   global_ts_ = global_ts;
 }
 

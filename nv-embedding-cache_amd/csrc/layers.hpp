@@ -180,6 +180,23 @@ class GpuTable {
   // runs on stream s (the modify stream or the table's private stream)
   void modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
                      const uint8_t* rows, int64_t row_stride, bool from_uvm);
+  // modify_on_gpu = false (CacheSAHostModify): the policy runs on the host
+  // over a host copy of the tags and the counters, then the chosen ways go
+  // through the same invalidate -> drain -> copy -> commit kernels
+  void host_modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
+                          const uint8_t* rows, int64_t row_stride, bool from_uvm);
+  // records (slot = set*8 + way, new tag, source row) to the device; with
+  // invalidate_only the ways are emptied and nothing is copied
+  void apply_records(ExecutionContext& ctx, hipStream_t s, const std::vector<uint64_t>& slot,
+                     const std::vector<int64_t>& tag, const std::vector<uint64_t>& src,
+                     bool invalidate_only);
+  int64_t h_tag(uint64_t slot) const;
+  void set_h_tag(uint64_t slot, int64_t tag);
+  // ec_hash.h:36-60 on the host (unsigned arithmetic in the key's width)
+  int64_t load_key(const uint8_t* keys, int64_t i) const;
+  uint64_t set_of(int64_t key) const;
+  int64_t tag_of(int64_t key) const;
+  int64_t key_of(int64_t tag, uint64_t set) const;
   // lookup modes over the backing table (gpu_table.cu:271-287): the direct
   // lookup, SortGather (misses and hits sorted apart) and PipelineGather
   // (host threads copy the missed rows); all write the same output
@@ -199,6 +216,11 @@ class GpuTable {
   float* counters_ = nullptr;
   int64_t* set_ts_ = nullptr;
   int64_t global_ts_ = 0;
+  // host policy state (modify_on_gpu = false): a copy of the device tags kept
+  // in step by every modify, the way counters and the set timestamps
+  std::vector<uint8_t> h_tags_;
+  std::vector<float> h_counters_;
+  std::vector<int64_t> h_set_ts_;
   float decay_rate_ = 0.95f;  // EmbedCacheSA::CacheConfig default (ec_set_associative.h:120)
   float* decay_table_ = nullptr;
   int64_t decay_len_ = 0;

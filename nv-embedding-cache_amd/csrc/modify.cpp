@@ -80,7 +80,10 @@ void GpuTable::insert(ExecutionContext& ctx, int64_t n, const void* keys, int64_
   StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
   const void* d_vals = device_input(ctx, "insert_values", values,
                                     (size_t)(n - 1) * value_stride + value_size, q.stream);
-  modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
+  if (cfg_.modify_on_gpu)
+    modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
+  else
+    host_modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(d_vals), value_stride, false);
 }
 
 void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* keys) {
@@ -89,8 +92,11 @@ void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* key
   if (n <= 0) return;
   NVE_CHECK_ARG(keys != nullptr, "keys must not be null");
   StreamQueue q(ctx.modify_stream(), cfg_.private_stream);
-  modify_insert(ctx, q.stream, n, keys, static_cast<const uint8_t*>(cfg_.uvm_table),
-                cfg_.row_size_in_bytes, true);
+  const uint8_t* rows = static_cast<const uint8_t*>(cfg_.uvm_table);
+  if (cfg_.modify_on_gpu)
+    modify_insert(ctx, q.stream, n, keys, rows, cfg_.row_size_in_bytes, true);
+  else
+    host_modify_insert(ctx, q.stream, n, keys, rows, cfg_.row_size_in_bytes, true);
 }
 
 void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,

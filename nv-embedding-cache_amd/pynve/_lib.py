@@ -151,6 +151,7 @@ SIGNATURES = {
     "nve_amd_gpu_table_export_state": (I32, [P, P, P, P, PI64]),
     "nve_amd_gpu_table_import_state": (I32, [P, P, P, P, I64]),
     "nve_amd_gpu_table_data": (I32, [P, PP]),
+    "nve_amd_table_insert_from_uvm": (I32, [P, P, I64, P]),
 }
 
 _lib = None

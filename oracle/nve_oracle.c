@@ -566,10 +566,24 @@ uint64_t orc_cache_num_sets(uint64_t cache_bytes, int64_t row_bytes, int key_byt
   return cache_bytes / per;
 }
 
+/* ec_set_associative.h:677-683 with get_counter_size_per_set() == 0: the
+ * host-metadata cache keeps its counters in host memory. */
+uint64_t orc_cache_num_sets_host(uint64_t cache_bytes, int64_t row_bytes, int key_bytes) {
+  const uint64_t per = align16((uint64_t)key_bytes * ORC_WAYS) + align16((uint64_t)row_bytes * ORC_WAYS);
+  return cache_bytes / per;
+}
+
 int orc_cache_init(orc_cache* c, uint64_t cache_bytes, int64_t row_bytes, int key_bytes,
                    int64_t sentinel) {
+  return orc_cache_init_ex(c, cache_bytes, row_bytes, key_bytes, sentinel, 0);
+}
+
+int orc_cache_init_ex(orc_cache* c, uint64_t cache_bytes, int64_t row_bytes, int key_bytes,
+                      int64_t sentinel, int host_modify) {
   memset(c, 0, sizeof(*c));
-  c->num_sets = orc_cache_num_sets(cache_bytes, row_bytes, key_bytes);
+  c->host_modify = host_modify ? 1 : 0;
+  c->num_sets = host_modify ? orc_cache_num_sets_host(cache_bytes, row_bytes, key_bytes)
+                            : orc_cache_num_sets(cache_bytes, row_bytes, key_bytes);
   if (c->num_sets == 0) return -1;
   c->row_bytes = row_bytes;
   c->key_bytes = key_bytes;
@@ -947,6 +961,149 @@ int64_t orc_cache_erase(orc_cache* c, const void* keys, int64_t n) {
     }
   }
   return cnt;
+}
+
+void orc_cache_clear(orc_cache* c) {
+  const uint64_t ways = c->num_sets * ORC_WAYS;
+  for (uint64_t i = 0; i < ways; i++) c->tags[i] = c->sentinel;
+  if (c->host_modify) memset(c->counters, 0, sizeof(float) * ways);
+  memset(c->set_ts, 0, sizeof(int64_t) * c->num_sets);
+  c->global_ts = 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* host-metadata insert (modify_on_gpu = false)                              */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+  int64_t key;
+  int64_t first; /* first position, also the bin's creation order */
+  int64_t count;
+} host_bin;
+
+static int cmp_host_bin_key(const void* a, const void* b) {
+  const host_bin* x = (const host_bin*)a;
+  const host_bin* y = (const host_bin*)b;
+  if (x->key != y->key) return x->key < y->key ? -1 : 1;
+  return x->first < y->first ? -1 : (x->first > y->first);
+}
+
+/* count descending; equal counts in order of first occurrence */
+static int cmp_host_bin_count(const void* a, const void* b) {
+  const host_bin* x = (const host_bin*)a;
+  const host_bin* y = (const host_bin*)b;
+  if (x->count != y->count) return x->count > y->count ? -1 : 1;
+  return x->first < y->first ? -1 : (x->first > y->first);
+}
+
+/* embed_cache.h:199-229 */
+int64_t orc_histogram_host(const void* keys, int key_bytes, int64_t n, int64_t* ukeys,
+                           float* priority, int64_t* first_idx) {
+  if (n <= 0) return 0;
+  host_bin* b = (host_bin*)malloc(sizeof(host_bin) * (size_t)n);
+  for (int64_t i = 0; i < n; i++) {
+    b[i].key = load_key(keys, key_bytes, i);
+    b[i].first = i;
+    b[i].count = 1;
+  }
+  qsort(b, (size_t)n, sizeof(host_bin), cmp_host_bin_key);
+  int64_t u = 0;
+  for (int64_t i = 0; i < n; i++) {
+    if (u > 0 && b[u - 1].key == b[i].key) {
+      b[u - 1].count++; /* the bin keeps its first position */
+    } else {
+      b[u++] = b[i];
+    }
+  }
+  qsort(b, (size_t)u, sizeof(host_bin), cmp_host_bin_count);
+  for (int64_t i = 0; i < u; i++) {
+    ukeys[i] = b[i].key;
+    priority[i] = (float)b[i].count / (float)n; /* Bin::count is a float counting by 1 */
+    first_idx[i] = b[i].first;
+  }
+  free(b);
+  return u;
+}
+
+/* ec_set_associative_host_modify.h:218-296 plus modify() (:428-480): the tags
+ * and counters change on the host as candidates are visited; the recorded
+ * ways then get their rows copied and their tags committed. */
+int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* priority,
+                              const uint8_t* const* src_rows, int64_t m, int64_t max_update,
+                              int64_t* out_set, int64_t* out_way) {
+  const int64_t now = ++c->global_ts; /* advanced once per insert call */
+  const uint64_t ways = c->num_sets * ORC_WAYS;
+  /* one record per (set, way) in this call: the reference's insertMap */
+  int64_t* rec_of_slot = (int64_t*)malloc(sizeof(int64_t) * ways);
+  for (uint64_t i = 0; i < ways; i++) rec_of_slot[i] = -1;
+  int64_t cap = max_update < m ? max_update : m;
+  if (cap < 1) cap = 1;
+  uint64_t* rslot = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)cap);
+  const uint8_t** rsrc = (const uint8_t**)malloc(sizeof(uint8_t*) * (size_t)cap);
+  int64_t nrec = 0;
+  for (int64_t i = 0; i < m && nrec < max_update; i++) {
+    int64_t key = ukeys[i];
+    if (c->key_bytes == 4) key = (int64_t)(int32_t)key;
+    const uint32_t set = orc_cache_set(c, key);
+    int64_t* st = c->tags + (uint64_t)set * ORC_WAYS;
+    float* sc = c->counters + (uint64_t)set * ORC_WAYS;
+    if (c->set_ts[set] != now) {
+      const int64_t delta = now - c->set_ts[set];
+      const float f = (float)pow((double)c->decay_rate, (double)delta);
+      for (int w = 0; w < ORC_WAYS; w++) sc[w] *= f;
+      c->set_ts[set] = now;
+    }
+    int hit = 0;
+    for (int w = 0; w < ORC_WAYS; w++) {
+      if (orc_cache_key_of(c, st[w], set) == key) {
+        sc[w] += priority[i];
+        hit = 1;
+        break;
+      }
+    }
+    if (hit) continue;
+    int wmin = 0; /* std::min_element: the first smallest counter */
+    for (int w = 1; w < ORC_WAYS; w++)
+      if (sc[w] < sc[wmin]) wmin = w;
+    if (sc[wmin] > priority[i]) continue;
+    const uint64_t slot = (uint64_t)set * ORC_WAYS + (uint64_t)wmin;
+    if (rec_of_slot[slot] >= 0) continue;
+    sc[wmin] = priority[i];
+    st[wmin] = orc_cache_tag(c, key);
+    rec_of_slot[slot] = nrec;
+    rslot[nrec] = slot;
+    rsrc[nrec] = src_rows ? src_rows[i] : NULL;
+    nrec++;
+  }
+  for (int64_t r = 0; r < nrec; r++) {
+    if (rsrc[r])
+      memcpy(c->data + rslot[r] * (uint64_t)c->row_bytes, rsrc[r], (size_t)c->row_bytes);
+    if (out_set) out_set[r] = (int64_t)(rslot[r] / ORC_WAYS);
+    if (out_way) out_way[r] = (int64_t)(rslot[r] % ORC_WAYS);
+  }
+  free(rsrc);
+  free(rslot);
+  free(rec_of_slot);
+  return nrec;
+}
+
+int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
+                                   const uint8_t* values, int64_t value_stride,
+                                   int64_t max_modify_size) {
+  if (n <= 0) return 0;
+  int64_t* uk = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  float* pr = (float*)malloc(sizeof(float) * (size_t)n);
+  int64_t* fi = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  const int64_t u = orc_histogram_host(keys, c->key_bytes, n, uk, pr, fi);
+  const uint8_t** rows = (const uint8_t**)malloc(sizeof(uint8_t*) * (size_t)u);
+  for (int64_t i = 0; i < u; i++)
+    rows[i] = uvm ? uvm + (uint64_t)uk[i] * (uint64_t)c->row_bytes : values + fi[i] * value_stride;
+  const int64_t r = orc_cache_insert_host(c, uk, pr, rows, u, max_modify_size, NULL, NULL);
+  free(rows);
+  free(fi);
+  free(pr);
+  free(uk);
+  return r;
 }
 
 /* ------------------------------------------------------------------------- */

@@ -26,6 +26,12 @@
  *   orc_histogram                        brute force (collections.Counter)
  *   orc_cache_insert                     hand-derived cases of the 8-lane
  *                                        bitonic networks, invariants
+ *   orc_histogram_host                   brute force (stable sort of
+ *                                        collections.Counter by count)
+ *   orc_cache_insert_host                hand-derived cases (fill order,
+ *                                        >= replacement, one record per way,
+ *                                        decay closed form, stale counters
+ *                                        after erase, truncation)
  *   orc_dedup                            sorted/unique/inverse round trip
  * Parity unpinned: orc_cache_insert's decay factor is defined here as
  * (float)pow((double)rate, (double)delta); the reference uses CUDA __powf,
@@ -42,7 +48,7 @@ extern "C" {
 #endif
 
 /* dtype ids follow nve_c_api.h (values 1..10) plus the two extension row
- * formats of the MI355X build (see include/nve_c_api_ext.h). */
+ * formats of the MI355X build (see include/nve_amd_ext.h). */
 enum {
   ORC_F32 = 1,
   ORC_F16 = 3,
@@ -125,11 +131,17 @@ typedef struct orc_cache {
   int64_t* tags;     /* num_sets*8, value of the TagT (sign-extended for int32) */
   float* counters;   /* num_sets*8 */
   int64_t* set_ts;   /* num_sets */
+  int host_modify;   /* 1: CacheSAHostModify (modify_on_gpu = false), 0: device modify */
 } orc_cache;
 
 uint64_t orc_cache_num_sets(uint64_t cache_bytes, int64_t row_bytes, int key_bytes);
+/* host-metadata variant: the way counters live in host memory, so a set costs
+ * only its tags and rows (ec_set_associative.h:677-683, no counter term) */
+uint64_t orc_cache_num_sets_host(uint64_t cache_bytes, int64_t row_bytes, int key_bytes);
 int orc_cache_init(orc_cache* c, uint64_t cache_bytes, int64_t row_bytes, int key_bytes,
                    int64_t sentinel);
+int orc_cache_init_ex(orc_cache* c, uint64_t cache_bytes, int64_t row_bytes, int key_bytes,
+                      int64_t sentinel, int host_modify);
 void orc_cache_free(orc_cache* c);
 uint32_t orc_cache_set(const orc_cache* c, int64_t key);
 int64_t orc_cache_tag(const orc_cache* c, int64_t key);
@@ -162,6 +174,38 @@ int64_t orc_cache_insert_keys(orc_cache* c, const void* keys, int64_t n, const u
 
 /* Invalidate (erase) keys: every way whose key matches gets the sentinel tag. */
 int64_t orc_cache_erase(orc_cache* c, const void* keys, int64_t n);
+
+/* clear_cache: every tag empty, set timestamps and the insert clock back to 0
+ * (ec_set_associative_device_modify.cuh:205-222); the host-metadata cache also
+ * zeroes its counters (ec_set_associative_host_modify.h:192-211). */
+void orc_cache_clear(orc_cache* c);
+
+/* CPU DefaultHistogram (embed_cache.h:188-229): unique keys in order of first
+ * occurrence, then sorted by count descending; priority = float(count) /
+ * float(n) (a division); first_idx = first position of the key.  The reference
+ * sorts with std::sort, which leaves the order of equal counts unspecified;
+ * here equal counts keep first-occurrence order (a stable sort).  Returns
+ * #unique. */
+int64_t orc_histogram_host(const void* keys, int key_bytes, int64_t n, int64_t* ukeys,
+                           float* priority, int64_t* first_idx);
+
+/* CacheSAHostModify::insert (ec_set_associative_host_modify.h:218-296): the
+ * sequential policy of modify_on_gpu = false.  Candidates in histogram order;
+ * a set is decayed by (float)pow((double)rate, (double)delta) on its first
+ * touch of the call; a resident key adds its priority to its way; otherwise the
+ * first way with the smallest counter is replaced when priority >= that
+ * counter and that way was not already replaced in this call.  Stops once
+ * max_update records exist.  Writes (set, way) records if out_set/out_way are
+ * non-NULL; returns their count. */
+int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* priority,
+                              const uint8_t* const* src_rows, int64_t m, int64_t max_update,
+                              int64_t* out_set, int64_t* out_way);
+
+/* Convenience for the host-metadata cache: orc_histogram_host + insert, rows
+ * from a dense table when uvm != NULL, else values + first_idx*stride. */
+int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
+                                   const uint8_t* values, int64_t value_stride,
+                                   int64_t max_modify_size);
 
 /* ---- dedup (deduper.cuh:136-221) ----
  * unique: ascending unique keys; counts; inverse: positions sorted stably by key

@@ -52,6 +52,7 @@ class OrcCache(ctypes.Structure):
         ("tags", ctypes.c_void_p),
         ("counters", ctypes.c_void_p),
         ("set_ts", ctypes.c_void_p),
+        ("host_modify", ctypes.c_int),
     ]
 
 
@@ -78,6 +79,17 @@ def _declare(L):
     L.orc_cache_init.restype = I32
     L.orc_cache_init.argtypes = [ctypes.POINTER(OrcCache), U64, I64, I32, I64]
     L.orc_cache_free.argtypes = [ctypes.POINTER(OrcCache)]
+    L.orc_cache_num_sets_host.restype = U64
+    L.orc_cache_num_sets_host.argtypes = [U64, I64, I32]
+    L.orc_cache_init_ex.restype = I32
+    L.orc_cache_init_ex.argtypes = [ctypes.POINTER(OrcCache), U64, I64, I32, I64, I32]
+    L.orc_cache_clear.argtypes = [ctypes.POINTER(OrcCache)]
+    L.orc_histogram_host.restype = I64
+    L.orc_histogram_host.argtypes = [P, I32, I64, P, P, P]
+    L.orc_cache_insert_host.restype = I64
+    L.orc_cache_insert_host.argtypes = [ctypes.POINTER(OrcCache), P, P, P, I64, I64, P, P]
+    L.orc_cache_insert_keys_host.restype = I64
+    L.orc_cache_insert_keys_host.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, P, I64, I64]
     L.orc_cache_set.restype = ctypes.c_uint32
     L.orc_cache_set.argtypes = [ctypes.POINTER(OrcCache), I64]
     L.orc_cache_tag.restype = I64
@@ -221,11 +233,15 @@ def host_layer_lookup(keys, table_bytes, num_rows, row_bytes, dtype, pooling, sp
 
 
 class Cache:
-    """Model of the 8-way set-associative GPU cache (EmbedCacheSA<K,K> + device modify)."""
+    """Model of the 8-way set-associative GPU cache: EmbedCacheSA<K,K> with the
+    device-modify policy, or with the host-metadata policy (modify_on_gpu =
+    false) when host_modify is set."""
 
-    def __init__(self, cache_bytes, row_bytes, key_bytes=8, sentinel=-1):
+    def __init__(self, cache_bytes, row_bytes, key_bytes=8, sentinel=-1, host_modify=False):
         self.c = OrcCache()
-        rc = lib().orc_cache_init(ctypes.byref(self.c), cache_bytes, row_bytes, key_bytes, sentinel)
+        self.host_modify = bool(host_modify)
+        rc = lib().orc_cache_init_ex(ctypes.byref(self.c), cache_bytes, row_bytes, key_bytes, sentinel,
+                                     1 if host_modify else 0)
         if rc != 0:
             raise ValueError("cache too small")
         self.row_bytes = row_bytes
@@ -279,9 +295,28 @@ class Cache:
         return rows, hits, misses
 
     def insert_keys(self, keys, uvm=None, values=None, value_stride=0, max_modify_size=1 << 20):
+        """GpuTable::insert / insert_from_uvm with this cache's policy."""
         keys = np.ascontiguousarray(keys, self.kdt)
-        return lib().orc_cache_insert_keys(ctypes.byref(self.c), _p(keys), keys.size, _p(uvm),
-                                           _p(values), value_stride, max_modify_size)
+        fn = lib().orc_cache_insert_keys_host if self.host_modify else lib().orc_cache_insert_keys
+        return fn(ctypes.byref(self.c), _p(keys), keys.size, _p(uvm), _p(values), value_stride,
+                  max_modify_size)
+
+    def insert_hist_host(self, ukeys, priority, src_ptrs=None, max_update=1 << 20):
+        """The host-metadata policy over an already-built histogram; returns
+        the (set, way) records."""
+        ukeys = np.ascontiguousarray(ukeys, np.int64)
+        priority = np.ascontiguousarray(priority, np.float32)
+        m = ukeys.size
+        if src_ptrs is not None:
+            src_ptrs = np.ascontiguousarray(src_ptrs, np.uint64)
+        s = np.zeros(max(m, 1), np.int64)
+        w = np.zeros(max(m, 1), np.int64)
+        n = lib().orc_cache_insert_host(ctypes.byref(self.c), _p(ukeys), _p(priority), _p(src_ptrs), m,
+                                        max_update, _p(s), _p(w))
+        return s[:n], w[:n]
+
+    def clear(self):
+        lib().orc_cache_clear(ctypes.byref(self.c))
 
     def insert_hist(self, ukeys, priority, src_ptrs):
         ukeys = np.ascontiguousarray(ukeys, np.int64)
@@ -299,8 +334,21 @@ class Cache:
         return lib().orc_cache_erase(ctypes.byref(self.c), _p(keys), keys.size)
 
 
-def cache_num_sets(cache_bytes, row_bytes, key_bytes=8):
+def cache_num_sets(cache_bytes, row_bytes, key_bytes=8, host_modify=False):
+    if host_modify:
+        return lib().orc_cache_num_sets_host(cache_bytes, row_bytes, key_bytes)
     return lib().orc_cache_num_sets(cache_bytes, row_bytes, key_bytes)
+
+
+def histogram_host(keys):
+    """CPU DefaultHistogram order (first occurrence, stable by count desc)."""
+    keys = np.ascontiguousarray(keys)
+    n = keys.size
+    uk = np.zeros(max(n, 1), np.int64)
+    pr = np.zeros(max(n, 1), np.float32)
+    fi = np.zeros(max(n, 1), np.int64)
+    u = lib().orc_histogram_host(_p(keys), keys.itemsize, n, _p(uk), _p(pr), _p(fi))
+    return uk[:u], pr[:u], fi[:u]
 
 
 def histogram(keys):

@@ -25,7 +25,7 @@ class CachedTable:
     from an oracle cache model."""
 
     def __init__(self, uvm_bytes, cache_bytes, key_bytes=8, with_uvm=True, value_dtype=_lib.DT_F32,
-                 kernel_mode_type=0, kernel_mode_value=0):
+                 kernel_mode_type=0, kernel_mode_value=0, modify_on_gpu=True, max_modify_size=None):
         self.rows, self.width = uvm_bytes.shape
         self.key_bytes = key_bytes
         self.uvm_np = np.ascontiguousarray(uvm_bytes)
@@ -37,6 +37,9 @@ class CachedTable:
         cfg.value_dtype = value_dtype
         cfg.kernel_mode_type = kernel_mode_type
         cfg.kernel_mode_value = kernel_mode_value
+        cfg.modify_on_gpu = 1 if modify_on_gpu else 0
+        if max_modify_size is not None:
+            cfg.max_modify_size = max_modify_size
         if with_uvm:
             cfg.uvm_table = self.h_uvm.data_ptr()
             cfg.uvm_num_rows = self.rows
@@ -49,7 +52,7 @@ class CachedTable:
         ns = ctypes.c_int64()
         _lib.call("nve_amd_gpu_table_num_sets", self.table, ctypes.byref(ns))
         self.num_sets = ns.value
-        self.model = O.Cache(cache_bytes, self.width, key_bytes)
+        self.model = O.Cache(cache_bytes, self.width, key_bytes, host_modify=not modify_on_gpu)
         assert self.model.num_sets == self.num_sets
 
     def load_model(self):
