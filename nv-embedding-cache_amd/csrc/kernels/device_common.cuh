@@ -236,22 +236,38 @@ __device__ __forceinline__ float ld_f32_unaligned(const uint8_t* p) {
   return __uint_as_float(v);
 }
 
-template <int SDT>
-__device__ __forceinline__ Meta load_meta(const uint8_t* row, int64_t value_bytes) {
+// MW: the metadata is aligned to its own size (4 or 8 bytes) in every row, so
+// it comes with one load; otherwise it is assembled from 16-bit loads.
+template <int SDT, bool MW = false>
+__device__ __forceinline__ Meta load_meta(uint64_t row, int64_t value_bytes) {
   Meta m{1.0f, 0.0f};
-  const uint8_t* p = row + value_bytes;
-  if constexpr (SDT == kQI8F32 || SDT == kXE4M3F32) {
-    m.s = ld_f32_unaligned(p);
+  const uint64_t p = row + (uint64_t)value_bytes;
+  if constexpr (MW && (SDT == kQU8F32 || SDT == kXI8AF32)) {
+    const u32x2 x = gload<u32x2>(p);
+    m.s = __uint_as_float(x.x);
+    m.o = __uint_as_float(x.y);
+  } else if constexpr (MW && (SDT == kQI8F32 || SDT == kXE4M3F32)) {
+    m.s = __uint_as_float(gload<uint32_t>(p));
+  } else if constexpr (MW && SDT == kQU8F16) {
+    const uint32_t x = gload<uint32_t>(p);
+    m.s = h2f((uint16_t)(x & 0xffffu));
+    m.o = h2f((uint16_t)(x >> 16));
+  } else if constexpr (SDT == kQI8F32 || SDT == kXE4M3F32) {
+    m.s = ld_f32_unaligned(reinterpret_cast<const uint8_t*>(p));
   } else if constexpr (SDT == kQU8F32 || SDT == kXI8AF32) {
-    m.s = ld_f32_unaligned(p);
-    m.o = ld_f32_unaligned(p + 4);
+    m.s = ld_f32_unaligned(reinterpret_cast<const uint8_t*>(p));
+    m.o = ld_f32_unaligned(reinterpret_cast<const uint8_t*>(p + 4));
   } else if constexpr (SDT == kQI8F16) {
-    m.s = h2f(gload<uint16_t>((uint64_t)p));
+    m.s = h2f(gload<uint16_t>(p));
   } else if constexpr (SDT == kQU8F16) {
-    m.s = h2f(gload<uint16_t>((uint64_t)p));
-    m.o = h2f(gload<uint16_t>((uint64_t)p + 2));
+    m.s = h2f(gload<uint16_t>(p));
+    m.o = h2f(gload<uint16_t>(p + 2));
   }
   return m;
+}
+template <int SDT>
+__device__ __forceinline__ Meta load_meta(const uint8_t* row, int64_t value_bytes) {
+  return load_meta<SDT, false>((uint64_t)row, value_bytes);
 }
 
 // Decoded element formulas (kernels_common.cuh:174-297):

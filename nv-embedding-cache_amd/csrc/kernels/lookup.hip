@@ -17,26 +17,39 @@
 
 namespace nve_amd {
 
-constexpr int kUnroll = 8;
-
 // ---------------------------------------------------------------------------
 // gather: one output row per key (raw bytes or dequantized values)
+//
+// U row loads per lane group are issued before any is used; a key that
+// resolves to no row (hit-mask skip, cache miss without a backing table, past
+// the end of the keys) reads the zero row, so no load sits behind a branch and
+// nothing is stored for it.  MW: the row's quantization metadata is aligned to
+// its own size, so scale (and offset) come with one load.
 // ---------------------------------------------------------------------------
-template <int SDT, int VB, bool RAW>
-__global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift, int passes) {
+template <int SDT, int VB, bool RAW, int U, bool MW>
+__global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift, int t_shift,
+                                                     int passes) {
   constexpr int ES = RAW ? 1 : Fmt<SDT>::esize;
   constexpr int E = VB / ES;
+  // a wave resolves T = 2^t_shift keys (T <= 64): enough for each lane group
+  // to move its share in one batch of U loads, so narrow launches still have
+  // many waves and every wave one round trip
+  const int T = 1 << t_shift;
   const int lane = threadIdx.x & 63;
   const int64_t tile = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t i = tile * 64 + lane;
-  const bool valid = i < a.n;
+  const int64_t base = tile << t_shift;
+  const int64_t i = base + lane;
+  const bool valid = lane < T && i < a.n;
 
   // ---- resolve: one key per lane ----
+  // hit-mask words cover 64 keys; a wave owns bits [sub, sub + T) of its word
+  const int64_t word = base >> 6;
+  const int sub = (int)(base & 63);
   uint64_t in_word = 0;
   bool skip = false;
-  if (a.hitmask != nullptr && tile * 64 < a.n) {
-    in_word = a.hitmask[tile];
-    skip = (in_word >> lane) & 1u;
+  if (a.hitmask != nullptr && base < a.n) {
+    in_word = a.hitmask[word];
+    skip = lane < T && ((in_word >> (sub + lane)) & 1u);
   }
   uint64_t addr = 0;
   bool miss = false;
@@ -47,8 +60,14 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
     if (a.out_index != nullptr) orow = a.out_index[i];
   }
   if (a.hitmask != nullptr) {
-    const uint64_t hits = __ballot(addr != 0);
-    if (lane == 0 && tile * 64 < a.n) a.hitmask[tile] = in_word | hits;
+    const uint64_t hits = __ballot(addr != 0);  // lanes >= T never resolve
+    if (lane == 0 && base < a.n) {
+      if (T == 64)
+        a.hitmask[word] = in_word | hits;
+      else if (hits)  // other waves own the word's other bits
+        atomicOr(reinterpret_cast<unsigned long long*>(a.hitmask + word),
+                 (unsigned long long)(hits << sub));
+    }
   }
   if (a.miss_counter != nullptr) add_misses(a.miss_counter, miss ? 1u : 0u);
 
@@ -57,41 +76,48 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherLaunch a, int g_shift
   const int gl = lane & (G - 1);
   const int grp = lane >> g_shift;
   const int groups = 64 >> g_shift;
+  const int per_group = T >> (6 - g_shift) > 0 ? T >> (6 - g_shift) : 1;  // keys per group
   const int64_t area = RAW ? (int64_t)a.src.row_bytes : a.count * ES;
-  const int out_es = (a.out_dtype == kF16) ? 2 : 4;
+  const bool out_f16 = a.out_dtype == kF16;
+  const int out_es = out_f16 ? 2 : 4;
+  const uint64_t zero_row = (uint64_t)g_zero_row;
   uint8_t* out = reinterpret_cast<uint8_t*>(a.out);
   for (int p = 0; p < passes; ++p) {
     const int64_t off = ((int64_t)p * G + gl) * VB;
     const bool in_row = off < area;
-    for (int q0 = 0; q0 < G; q0 += kUnroll) {
-      Vec<VB> v[kUnroll];
-      Meta m[kUnroll];
-      uint64_t ra[kUnroll];
-      uint32_t orw[kUnroll];
+    for (int q0 = 0; q0 < per_group; q0 += U) {
+      uint64_t ra[U];
+      uint32_t orw[U];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int q = q0 + u;
-        const int j = grp + (q < G ? q : 0) * groups;
+        const int j = grp + (q < per_group ? q : 0) * groups;
         ra[u] = shfl64(addr, j);
         orw[u] = a.out_index != nullptr ? shfl32(orow, j) : 0u;
-        if (q >= G) ra[u] = 0;
-        if (ra[u] != 0 && in_row) v[u] = load_vec<VB>(reinterpret_cast<const uint8_t*>(ra[u]) + off);
-        if constexpr (!RAW && Fmt<SDT>::meta != 0) {
-          if (ra[u] != 0) m[u] = load_meta<SDT>(reinterpret_cast<const uint8_t*>(ra[u]), area);
-        }
+        if (q >= per_group) ra[u] = 0;
+      }
+      Vec<VB> v[U];
+      Meta m[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool real = ra[u] != 0;
+        const uint64_t row = real ? ra[u] : zero_row;
+        v[u] = load_vec<VB>(row + ((real && in_row) ? off : (off & kZeroRowMask)));
+        if constexpr (!RAW && Fmt<SDT>::meta != 0)
+          m[u] = load_meta<SDT, MW>(row, real ? area : (area & kZeroRowMask));
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+      for (int u = 0; u < U; ++u) {
         if (ra[u] == 0 || !in_row) continue;
         const int64_t row = a.out_index != nullptr ? (int64_t)orw[u]
-                                                   : tile * 64 + grp + (int64_t)(q0 + u) * groups;
+                                                   : base + grp + (int64_t)(q0 + u) * groups;
         uint8_t* o = out + row * a.out_stride;
         if constexpr (RAW) {
           store_vec<VB>(o + off, v[u]);
         } else {
           float x[E];
           decode<SDT, VB>(v[u], m[u], x);
-          store_out<E>(o + ((int64_t)p * G + gl) * E * out_es, x, a.out_dtype == kF16);
+          store_out<E>(o + ((int64_t)p * G + gl) * E * out_es, x, out_f16);
         }
       }
     }
@@ -223,20 +249,57 @@ hipError_t launch_gather(const GatherLaunch& a, hipStream_t stream) {
   const int64_t nv = area / vb;
   const int g = nv >= 64 ? 64 : pow2_ceil(nv);
   const int passes = (int)((nv + g - 1) / g);
-  const int64_t waves = (a.n + 63) / 64;
+  const int gs = log2i(g);
+  // 16 loads in flight per lane group for rows of 16+ lane slices; a wave
+  // resolves groups * unroll keys (at most 64), one batch per group
+  const int unroll = g >= 16 ? 16 : 8;
+  const int tkeys = (64 / g) * unroll < 64 ? (64 / g) * unroll : 64;
+  const int ts = log2i(tkeys);
+  const int64_t waves = (a.n + tkeys - 1) / tkeys;
   const int threads = 256;
   const int64_t grid = (waves * 64 + threads - 1) / threads;
-  const int gs = log2i(g);
-#define L_RAW(V) hipLaunchKernelGGL((gather_kernel<kF16, V, true>), dim3(grid), dim3(threads), 0, stream, a, gs, passes)
-#define L_DQ(S, V) hipLaunchKernelGGL((gather_kernel<S, V, false>), dim3(grid), dim3(threads), 0, stream, a, gs, passes)
+  // metadata aligned to its own size in every row (cache rows included)
+  bool mw = false;
+  if (!a.raw) {
+    const int mb = meta_bytes(a.stored_dtype);
+    const int ma = (mb == 8) ? 8 : 4;
+    mw = mb >= 4 && area % ma == 0 && a.src.row_bytes % (uint64_t)ma == 0 &&
+         (!a.src.table || aligned(a.src.table, ma)) && (!a.src.cache_data || aligned(a.src.cache_data, ma));
+  }
+#define L_RAW(V)                                                                                  \
+  do {                                                                                            \
+    if (unroll == 16)                                                                             \
+      hipLaunchKernelGGL((gather_kernel<kF16, V, true, 16, false>), dim3(grid), dim3(threads), 0, \
+                         stream, a, gs, ts, passes);                                                  \
+    else                                                                                          \
+      hipLaunchKernelGGL((gather_kernel<kF16, V, true, 8, false>), dim3(grid), dim3(threads), 0,  \
+                         stream, a, gs, ts, passes);                                                  \
+  } while (0)
+#define L_DQ_U(S, V, M)                                                                           \
+  do {                                                                                            \
+    if (unroll == 16)                                                                             \
+      hipLaunchKernelGGL((gather_kernel<S, V, false, 16, M>), dim3(grid), dim3(threads), 0,       \
+                         stream, a, gs, ts, passes);                                                  \
+    else                                                                                          \
+      hipLaunchKernelGGL((gather_kernel<S, V, false, 8, M>), dim3(grid), dim3(threads), 0,        \
+                         stream, a, gs, ts, passes);                                                  \
+  } while (0)
+#define L_DQ(S, V)             \
+  do {                         \
+    if (mw)                    \
+      L_DQ_U(S, V, true);      \
+    else                       \
+      L_DQ_U(S, V, false);     \
+  } while (0)
+#define L_DQN(S, V) L_DQ_U(S, V, false)
   if (a.raw) {
     NVE_DISPATCH_VB(vb, L_RAW);
   } else {
     switch (a.stored_dtype) {
-#define C_F32(V) L_DQ(kF32, V)
-#define C_F16(V) L_DQ(kF16, V)
+#define C_F32(V) L_DQN(kF32, V)
+#define C_F16(V) L_DQN(kF16, V)
 #define C_QI8F32(V) L_DQ(kQI8F32, V)
-#define C_QI8F16(V) L_DQ(kQI8F16, V)
+#define C_QI8F16(V) L_DQN(kQI8F16, V)
 #define C_QU8F32(V) L_DQ(kQU8F32, V)
 #define C_QU8F16(V) L_DQ(kQU8F16, V)
 #define C_XI8A(V) L_DQ(kXI8AF32, V)
