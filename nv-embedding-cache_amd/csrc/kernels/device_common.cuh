@@ -328,6 +328,12 @@ __device__ __forceinline__ int64_t load_key(const void* keys, int key_bytes, int
                         : reinterpret_cast<const int64_t*>(keys)[i];
 }
 
+// per-key pooling weight (f32 or f16), indexed by the key's global position
+__device__ __forceinline__ float load_weight(const void* w, int wdt, int64_t k) {
+  return wdt == kF16 ? h2f(reinterpret_cast<const uint16_t*>(w)[k])
+                     : reinterpret_cast<const float*>(w)[k];
+}
+
 __device__ __forceinline__ void store_key(void* keys, int key_bytes, int64_t i, int64_t v) {
   if (key_bytes == 4)
     reinterpret_cast<int32_t*>(keys)[i] = (int32_t)v;

@@ -25,11 +25,6 @@
 
 namespace nve_amd {
 
-__device__ __forceinline__ float load_weight(const void* w, int wdt, int64_t k) {
-  return wdt == kF16 ? h2f(reinterpret_cast<const uint16_t*>(w)[k])
-                     : reinterpret_cast<const float*>(w)[k];
-}
-
 // ---------------------------------------------------------------------------
 // find-and-pool: one output row per bag
 // ---------------------------------------------------------------------------

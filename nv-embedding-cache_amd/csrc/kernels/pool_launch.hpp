@@ -14,4 +14,9 @@ hipError_t launch_pool_quant(const PoolLaunch& a, const PoolGeometry& g, hipStre
 // kXI8AF32, kXE4M3F32
 hipError_t launch_pool_ext(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
 
+// Long bags over one linear f16 / f32 table (pool_split.hip): the same sums
+// as pool_kernel's split-bag path with fewer instructions.
+bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g);
+hipError_t launch_pool_split(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
+
 }  // namespace nve_amd

@@ -1,0 +1,286 @@
+// pool_split.hip -- find-and-pool for long bags over a linear table: the
+// shape of the GPULayer benchmark (a few hundred bags of ~1K keys, rows of
+// 16-byte lane slices), where the general pool_kernel spends most of its time
+// on instructions rather than on memory.
+//
+// Reference behaviour restated: find_and_combine (cuda_ops/find_and_combine_kernel.cuh:40-154)
+// over a linear table (GPULayer, gpu_embedding_layer.cu:153-189).
+//
+// Same decomposition and summation order as pool_kernel's split-bag path, so
+// the two produce the same bits: one workgroup per bag, the bag cut into gpb
+// contiguous key chunks, one chunk per G-lane group, each group accumulating
+// its chunk in key order; an xor butterfly inside each wave; the waves'
+// partial rows added in wave order through LDS.  What is leaner:
+//  * row indices travel between lanes as 32 bits and by VALU lane moves, not
+//    LDS permutes: DPP row_newbcast inside a 16-lane row, v_permlane16_swap /
+//    v_permlane32_swap across rows (gfx950), v_readlane for a whole-wave
+//    group; the address is formed by the consuming lane;
+//  * the butterfly uses the same lane moves: a + (a of lane l ^ m), formed as
+//    the sum of the two swapped halves, which is the same float addition;
+//  * no cache / backing-table / multi-table / hit-mask branches, one pass per
+//    row (G * 16 bytes cover the row), G and the weighting fixed at compile
+//    time;
+//  * the cross-wave sum is unrolled so its LDS reads are all in flight.
+#include <type_traits>
+
+#include "device_common.cuh"
+#include "pool_launch.hpp"
+
+namespace nve_amd {
+
+namespace {
+
+constexpr uint32_t kNoRow = 0xffffffffu;
+
+// DPP controls (row = 16 lanes)
+constexpr int kDppRowNewBcast = 0x150;  // + n: every lane of a row reads lane n of that row
+constexpr int kDppRowRor8 = 0x128;      // lane l reads lane (l + 8) mod 16 of its row: l ^ 8
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+// Value of lane J of this lane's G-lane group (groups aligned to G lanes).
+template <int G, int J>
+__device__ __forceinline__ uint32_t group_bcast(uint32_t v, int lane) {
+  if constexpr (G == 64) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, J);
+  } else if constexpr (G == 16) {
+    return dpp_mov<kDppRowNewBcast + J>(v);
+  } else if constexpr (G == 8) {
+    const uint32_t lo = dpp_mov<kDppRowNewBcast + J>(v);
+    const uint32_t hi = dpp_mov<kDppRowNewBcast + 8 + J>(v);
+    return (lane & 8) ? hi : lo;
+  } else {  // G == 32: lane J % 16 of each row, then the even or odd row of each pair
+    const uint32_t b = dpp_mov<kDppRowNewBcast + (J & 15)>(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    return J < 16 ? r[0] : r[1];
+  }
+}
+
+// a + (a of lane l ^ M), the same float addition as a + __shfl_xor(a, M)
+// (addition commutes exactly, so both partners get the same bits).
+template <int M>
+__device__ __forceinline__ float xor_add(float a) {
+  if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    static_assert(M == 8, "lane groups of 8 to 64 lanes");
+    return a + __uint_as_float(dpp_mov<kDppRowRor8>(__float_as_uint(a)));
+  }
+}
+
+// ri[u] / wu[u] = lane J0 + u of the group, u < U (J0 + U <= G)
+template <int G, int U, bool W, int J0, int u = 0>
+__device__ __forceinline__ void group_bcast_batch(uint32_t ridx, float w, int lane, uint32_t* ri,
+                                                  float* wu) {
+  if constexpr (u < U) {
+    static_assert(J0 + u < G, "broadcast source outside the group");
+    ri[u] = group_bcast<G, J0 + u>(ridx, lane);
+    wu[u] = W ? __uint_as_float(group_bcast<G, J0 + u>(__float_as_uint(w), lane)) : 1.0f;
+    group_bcast_batch<G, U, W, J0, u + 1>(ridx, w, lane, ri, wu);
+  }
+}
+
+template <int G, int M = G>
+__device__ __forceinline__ void butterfly(float* acc, int e, float& wsum, bool weighted) {
+  if constexpr (M < 64) {
+    for (int c = 0; c < e; ++c) acc[c] = xor_add<M>(acc[c]);
+    if (weighted) wsum = xor_add<M>(wsum);
+    butterfly<G, 2 * M>(acc, e, wsum, weighted);
+  }
+}
+
+template <int SDT, int G, bool W>
+__global__ __launch_bounds__(1024) void pool_split_kernel(PoolLaunch a, int gpb_shift) {
+  constexpr int VB = 16;
+  constexpr int ES = Fmt<SDT>::esize;
+  constexpr int E = VB / ES;
+  constexpr int U = G < 16 ? G : 16;  // row loads in flight per lane; a group's keys in G / U batches
+  extern __shared__ float lds[];
+
+  const int tid = threadIdx.x;
+  const int gl = tid & (G - 1);
+  const int chunk = tid / G;
+  const int gpb = 1 << gpb_shift;
+  const int64_t bag = blockIdx.x;
+
+  int64_t s, e;
+  if (a.offsets != nullptr) {
+    s = load_key(a.offsets, a.key_bytes, bag);
+    e = load_key(a.offsets, a.key_bytes, bag + 1);
+    s = s < 0 ? 0 : (s > a.num_keys ? a.num_keys : s);
+    e = e < s ? s : (e > a.num_keys ? a.num_keys : e);
+  } else {
+    s = bag * a.hotness;
+    e = s + a.hotness;
+  }
+  int64_t cs = s, ce = e;
+  if (e > s) {
+    const int64_t per = (e - s + gpb - 1) >> gpb_shift;
+    cs = s + chunk * per;
+    if (cs > e) cs = e;
+    ce = cs + per < e ? cs + per : e;
+  }
+
+  const uint64_t table = (uint64_t)a.src.table;
+  const uint64_t row_bytes = a.src.row_bytes;
+  const uint64_t num_rows = a.src.num_rows;
+  const uint64_t zero_row = (uint64_t)g_zero_row;
+  const int64_t value_bytes = a.count * ES;
+  const int off = gl * VB;
+  const bool in_row = off < value_bytes;
+
+  float acc[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) acc[c] = 0.0f;
+  float wsum = 0.0f;
+
+  const int lane = tid & 63;
+  for (int64_t k0 = cs; k0 < ce; k0 += G) {
+    const int64_t kk = k0 + gl;
+    uint32_t ridx = kNoRow;
+    float w = 0.0f;
+    if (kk < ce) {
+      const int64_t key = load_key(a.keys, a.key_bytes, kk);
+      if ((uint64_t)key < num_rows) ridx = (uint32_t)key;  // keys outside the table read nothing
+      if (W) w = load_weight(a.weights, a.weight_dtype, kk);
+    }
+    const int n = (int)((ce - k0) < G ? (ce - k0) : G);
+    // batch starting at key j0 of the group (compile time, so every lane move
+    // has an immediate source lane); lanes past the group's keys hold kNoRow:
+    // they load the zero row and are not added
+    auto batch = [&](auto jc) {
+      constexpr int j0 = decltype(jc)::value;
+      if (j0 >= n) return;
+      uint32_t ri[U];
+      float wu[U];
+      group_bcast_batch<G, U, W, j0>(ridx, w, lane, ri, wu);
+      Vec<VB> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool real = ri[u] != kNoRow && in_row;
+        const uint64_t addr = real ? table + (uint64_t)ri[u] * row_bytes + (uint64_t)off
+                                   : zero_row + (uint64_t)(off & kZeroRowMask);
+        v[u] = load_vec<VB>(addr);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool use = j0 + u < n;  // uniform over the group
+        if (W && use) wsum += wu[u];
+        const bool add = use && in_row && ri[u] != kNoRow;
+        float x[E];
+        Meta m{1.0f, 0.0f};
+        decode<SDT, VB>(v[u], m, x);
+#pragma unroll
+        for (int c = 0; c < E; ++c) {
+          const float t = W ? __builtin_fmaf(x[c], wu[u], acc[c]) : acc[c] + x[c];
+          acc[c] = add ? t : acc[c];
+        }
+      }
+    };
+    batch(std::integral_constant<int, 0>{});
+    if constexpr (G / U > 1) batch(std::integral_constant<int, U>{});
+    if constexpr (G / U > 2) {
+      batch(std::integral_constant<int, 2 * U>{});
+      batch(std::integral_constant<int, 3 * U>{});
+    }
+  }
+
+  // butterfly over the wave's groups (the same pairing and additions as pool_kernel)
+  butterfly<G>(acc, E, wsum, W);
+
+  // waves' partial rows, added in wave order
+  constexpr int row_elems = G * E;
+  const int wave = tid >> 6;
+  const int waves = (gpb * G) >> 6;
+  float* red = lds;
+  float* wred = lds + (blockDim.x >> 6) * row_elems;
+  if ((tid & 63) < G) {
+#pragma unroll
+    for (int c = 0; c < E; ++c) red[wave * row_elems + gl * E + c] = acc[c];
+    if (gl == 0) wred[wave] = wsum;
+  }
+  __syncthreads();
+  if (tid < row_elems && ((tid / E) * VB) < value_bytes) {
+    float part[16];
+    float wp[16];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      part[w] = w < waves ? red[w * row_elems + tid] : 0.0f;
+      wp[w] = (W && w < waves) ? wred[w] : 0.0f;
+    }
+    float v = part[0];
+    float ws = wp[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) {
+      if (w < waves) {
+        v += part[w];
+        ws += wp[w];
+      }
+    }
+    if (a.mean) {
+      const float d = W ? ws : (float)(e - s);
+      v = (d == 0.0f) ? 0.0f : v / d;
+    }
+    uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + bag * a.out_stride;
+    if (a.out_dtype == kF16)
+      *reinterpret_cast<gptr_w<uint16_t>>((uint64_t)o + (uint64_t)tid * 2) = f2h(v);
+    else
+      *reinterpret_cast<gptr_w<float>>((uint64_t)o + (uint64_t)tid * 4) = v;
+  }
+}
+
+template <int SDT, int G>
+hipError_t launch_split_g(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
+  const int ps = [](int x) {
+    int r = 0;
+    while ((1 << r) < x) ++r;
+    return r;
+  }(g.gpb);
+  const dim3 grid((unsigned)g.grid), block((unsigned)g.threads);
+  if (a.weighted)
+    hipLaunchKernelGGL((pool_split_kernel<SDT, G, true>), grid, block, g.lds_bytes, stream, a, ps);
+  else
+    hipLaunchKernelGGL((pool_split_kernel<SDT, G, false>), grid, block, g.lds_bytes, stream, a, ps);
+  return hipGetLastError();
+}
+
+template <int SDT>
+hipError_t launch_split_sdt(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
+  switch (g.g) {
+    case 8: return launch_split_g<SDT, 8>(a, g, stream);
+    case 16: return launch_split_g<SDT, 16>(a, g, stream);
+    case 32: return launch_split_g<SDT, 32>(a, g, stream);
+    case 64: return launch_split_g<SDT, 64>(a, g, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g) {
+  if (a.src.cache_data != nullptr || a.num_tables > 0 || !a.src.load_indices) return false;
+  if (a.src.table == nullptr || a.src.num_rows == 0 || a.src.num_rows >= kNoRow) return false;
+  if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
+  if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;
+  if (g.vb != 16 || g.passes != 1 || g.bags_per_wg != 1) return false;
+  if (g.g < 8 || g.g > 64 || g.gpb * g.g <= 64 || g.gpb * g.g > 1024) return false;
+  if (g.threads != g.gpb * g.g) return false;
+  // the cross-wave sum reads at most 16 waves' partials, one element per thread
+  const int row_elems = g.g * (16 / (a.stored_dtype == kF16 ? 2 : 4));
+  return row_elems <= g.threads;
+}
+
+hipError_t launch_pool_split(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
+  if (a.stored_dtype == kF16) return launch_split_sdt<kF16>(a, g, stream);
+  if (a.stored_dtype == kF32) return launch_split_sdt<kF32>(a, g, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace nve_amd

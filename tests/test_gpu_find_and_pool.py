@@ -175,3 +175,59 @@ def test_out_of_range_keys_read_as_zero_rows(dtype, split):
             assert pooled_f16_close(got.view(np.uint16), ref.view(np.uint16))
         else:
             assert rel_close(got, ref, 1e-5)
+
+
+@pytest.mark.parametrize("dtype,dim", [(O.F16, 64), (O.F16, 128), (O.F32, 128), (O.F16, 512), (O.F32, 256)])
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WSUM, _lib.POOL_WMEAN])
+@pytest.mark.parametrize("split", [0, 8, 64])
+def test_long_bag_kernel_matches_general_kernel_bitwise(dtype, dim, pooling, split):
+    """Long bags over a linear f16/f32 table take the lean split-bag kernel
+    (unroll hint 0); an unroll hint forces the general kernel.  Both cut a bag
+    into the same chunks and add them in the same order, so their outputs must
+    be identical bit for bit -- and within fp32 tolerance of the key-order
+    oracle.  Keys outside the table (read as nothing) are mixed in."""
+    rng = np.random.default_rng(1000 + dim + 7 * pooling + split)
+    rows, bags, hot = 30000, 40, 700
+    tb = float_table(rng, rows, dim, dtype, dyadic_values=False)
+    keys = rng.integers(0, rows, size=bags * hot).astype(np.int64)
+    keys[rng.uniform(size=keys.size) < 0.01] = rows + 5  # outside the table
+    weighted = pooling in (_lib.POOL_WSUM, _lib.POOL_WMEAN)
+    w = rng.uniform(0, 1, size=keys.size).astype(np.float32) if weighted else None
+    got = [run_pool(tb, dtype, keys, pooling, _lib.SPARSE_FIXED, None, bags, hot, w, O.F32, dtype, split, unroll)
+           for unroll in (0, 16, 8)]
+    bits = np.uint16 if dtype == O.F16 else np.uint32
+    assert np.array_equal(got[0].view(bits), got[1].view(bits))
+    assert np.array_equal(got[0].view(bits), got[2].view(bits))
+    padded = np.concatenate([tb, np.zeros((1, tb.shape[1]), np.uint8)])
+    mapped = np.where(keys < rows, keys, rows)
+    ref = oracle_pool(padded, mapped, dtype, dim, O.FIXED, pooling, None, bags, hot, w, O.F32, dtype)
+    if dtype == O.F16:
+        assert pooled_f16_close(got[0].view(np.uint16), ref.view(np.uint16))
+    else:
+        assert rel_close(got[0], ref, 1e-5)
+
+
+def test_long_bag_kernel_csr_empty_and_int32():
+    """CSR bags with empty and very long bags, int32 keys and offsets: the
+    lean kernel equals the general one bitwise and the oracle within fp32
+    tolerance (empty bags give zero rows)."""
+    rng = np.random.default_rng(77)
+    rows, dim, bags = 20000, 128, 64
+    tb = float_table(rng, rows, dim, O.F32, dyadic_values=False)
+    lens = rng.integers(500, 1500, size=bags)
+    lens[::9] = 0
+    off = np.zeros(bags + 1, np.int32)
+    off[1:] = np.cumsum(lens)
+    keys = rng.integers(0, rows, size=int(off[-1])).astype(np.int32)
+    res = []
+    for unroll in (0, 16):
+        out = torch.zeros((bags, dim), dtype=torch.float32, device="cuda")
+        fap(to_dev(keys), keys.size, to_dev(tb.reshape(-1)), rows, dim * 4, _lib.DT_F32, _lib.POOL_MEAN,
+            _lib.SPARSE_CSR, to_dev(off), off.size, 0, None, 0, _lib.DT_F32, out, dim * 4, 0, _lib.KEY_INT32,
+            unroll)
+        torch.cuda.synchronize()
+        res.append(out.cpu().numpy())
+    assert np.array_equal(res[0].view(np.uint32), res[1].view(np.uint32))
+    ref = oracle_pool(tb, keys, O.F32, dim, O.CSR, O.MEAN, off, bags, 0, None, 0, O.F32)
+    assert rel_close(res[0], ref, 1e-5)
+    assert np.all(res[0][lens == 0] == 0)
