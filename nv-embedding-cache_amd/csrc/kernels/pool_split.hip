@@ -96,8 +96,30 @@ __device__ __forceinline__ void butterfly(float* acc, int e, float& wsum, bool w
   }
 }
 
+// The kernel's arguments: only what this shape reads (PoolLaunch carries a
+// table array for multi-table launches; a smaller kernarg segment is quicker
+// to set up per launch).
+struct SplitArgs {
+  const void* keys;
+  const void* offsets;  // null: fixed hotness
+  const void* weights;
+  const uint8_t* table;
+  void* out;
+  int64_t num_keys;
+  int64_t hotness;
+  uint64_t row_bytes;
+  uint64_t num_rows;
+  int64_t count;
+  int64_t out_stride;
+  int key_bytes;
+  int weight_dtype;
+  int mean;
+  int out_dtype;
+  int gpb_shift;
+};
+
 template <int SDT, int G, bool W>
-__global__ __launch_bounds__(1024) void pool_split_kernel(PoolLaunch a, int gpb_shift) {
+__global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
   constexpr int VB = 16;
   constexpr int ES = Fmt<SDT>::esize;
   constexpr int E = VB / ES;
@@ -107,6 +129,7 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(PoolLaunch a, int gpb_
   const int tid = threadIdx.x;
   const int gl = tid & (G - 1);
   const int chunk = tid / G;
+  const int gpb_shift = a.gpb_shift;
   const int gpb = 1 << gpb_shift;
   const int64_t bag = blockIdx.x;
 
@@ -128,9 +151,9 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(PoolLaunch a, int gpb_
     ce = cs + per < e ? cs + per : e;
   }
 
-  const uint64_t table = (uint64_t)a.src.table;
-  const uint64_t row_bytes = a.src.row_bytes;
-  const uint64_t num_rows = a.src.num_rows;
+  const uint64_t table = (uint64_t)a.table;
+  const uint64_t row_bytes = a.row_bytes;
+  const uint64_t num_rows = a.num_rows;
   const uint64_t zero_row = (uint64_t)g_zero_row;
   const int64_t value_bytes = a.count * ES;
   const int off = gl * VB;
@@ -238,16 +261,29 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(PoolLaunch a, int gpb_
 
 template <int SDT, int G>
 hipError_t launch_split_g(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
-  const int ps = [](int x) {
-    int r = 0;
-    while ((1 << r) < x) ++r;
-    return r;
-  }(g.gpb);
+  SplitArgs s{};
+  s.keys = a.keys;
+  s.offsets = a.offsets;
+  s.weights = a.weights;
+  s.table = a.src.table;
+  s.out = a.out;
+  s.num_keys = a.num_keys;
+  s.hotness = a.hotness;
+  s.row_bytes = a.src.row_bytes;
+  s.num_rows = a.src.num_rows;
+  s.count = a.count;
+  s.out_stride = a.out_stride;
+  s.key_bytes = a.key_bytes;
+  s.weight_dtype = a.weight_dtype;
+  s.mean = a.mean;
+  s.out_dtype = a.out_dtype;
+  s.gpb_shift = 0;
+  while ((1 << s.gpb_shift) < g.gpb) ++s.gpb_shift;
   const dim3 grid((unsigned)g.grid), block((unsigned)g.threads);
   if (a.weighted)
-    hipLaunchKernelGGL((pool_split_kernel<SDT, G, true>), grid, block, g.lds_bytes, stream, a, ps);
+    hipLaunchKernelGGL((pool_split_kernel<SDT, G, true>), grid, block, g.lds_bytes, stream, s);
   else
-    hipLaunchKernelGGL((pool_split_kernel<SDT, G, false>), grid, block, g.lds_bytes, stream, a, ps);
+    hipLaunchKernelGGL((pool_split_kernel<SDT, G, false>), grid, block, g.lds_bytes, stream, s);
   return hipGetLastError();
 }
 
