@@ -530,7 +530,7 @@ def main():
     achieved = alg / (ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "pool_kernel<F16, VB=16, U=8, unweighted>", "alg_bytes_per_launch": alg}
+            "kernel": "pool_split_kernel<F16, G=16, unweighted>", "alg_bytes_per_launch": alg}
     tf = os.path.join(ROOT, "profiles", "c2pool_traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
