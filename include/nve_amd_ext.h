@@ -114,6 +114,31 @@ NVE_C_API nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out);
 NVE_C_API nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx,
                                                      int64_t n, const void* keys);
 
+/* Training backprop: the sparse gradient of a lookup with respect to the table
+ * (GradientCalculator::compute_gradients, cuda_ops/gradient_calculator.cuh:238-301,
+ * which the reference's pynve GPU bindings call as concat_backprop /
+ * pooling_backprop, python/pynve/bindings/binding_layers.hpp:131-250).
+ * pooling_type NVE_POOL_CONCATENATE: grads_in holds one row per key
+ * (num_keys rows); otherwise one row per bag (fixed_hotness, or
+ * num_csr_offsets - 1 bags of non-decreasing csr_offsets of the key type).
+ * grads_in / grads_out rows: embedding_width values of grad_type (FLOAT32 or
+ * FLOAT16); weights (WEIGHTED_*): one per key of weight_type FLOAT32 / FLOAT16.
+ * Sum weighs 1, WeightedSum w, Mean 1 / (keys in the bag), WeightedMean
+ * w / (the bag's weights added in order).  Outputs: the unique keys ascending
+ * (reserve num_keys entries of the key type), one gradient row per unique key
+ * (reserve num_keys rows) and *num_unique_out.  Sums are fp32 in a fixed order
+ * (each key's positions in runs of 64, then the runs) and rounded once, so the
+ * result is deterministic.  Device buffers and workspace; synchronizes the
+ * stream. */
+NVE_C_API nve_status_t nve_amd_backprop_workspace_size(int64_t num_keys, int64_t num_bags,
+                                                       int64_t embedding_width, uint64_t* bytes);
+NVE_C_API nve_status_t nve_amd_pooling_backprop(
+    nve_key_type_t key_type, int64_t num_keys, const void* keys, nve_pooling_type_t pooling_type,
+    nve_sparse_type_t sparse_type, const void* csr_offsets, int64_t num_csr_offsets,
+    int64_t fixed_hotness, const void* weights, nve_data_type_t weight_type, const void* grads_in,
+    nve_data_type_t grad_type, int64_t embedding_width, void* unique_keys_out, void* grads_out,
+    int64_t* num_unique_out, void* workspace, uint64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

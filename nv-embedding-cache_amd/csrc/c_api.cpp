@@ -9,6 +9,7 @@
 #include <new>
 
 #include "../../include/nve_amd_ext.h"
+#include "backprop.hpp"
 #include "dedup.hpp"
 #include "layers.hpp"
 
@@ -811,6 +812,48 @@ nve_status_t nve_amd_dedup(nve_key_type_t key_type, int64_t num_keys, const void
                   "keys and output buffers must not be NULL");
   *num_unique = dedup_run(key_bytes_of(key_type), num_keys, keys, unique_out, counts_out,
                           inverse_out, offsets_out, workspace, workspace_bytes, (hipStream_t)stream);
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_backprop_workspace_size(int64_t num_keys, int64_t num_bags,
+                                             int64_t embedding_width, uint64_t* bytes) {
+  C_TRY
+  NVE_CHECK_ARG(bytes != nullptr, "bytes must not be NULL");
+  NVE_CHECK_ARG(num_keys >= 0 && num_bags >= 0 && embedding_width > 0, "Invalid sizes");
+  *bytes = backprop_workspace_bytes(num_keys, num_bags, embedding_width);
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_pooling_backprop(nve_key_type_t key_type, int64_t num_keys, const void* keys,
+                                      nve_pooling_type_t pooling_type, nve_sparse_type_t sparse_type,
+                                      const void* csr_offsets, int64_t num_csr_offsets,
+                                      int64_t fixed_hotness, const void* weights,
+                                      nve_data_type_t weight_type, const void* grads_in,
+                                      nve_data_type_t grad_type, int64_t embedding_width,
+                                      void* unique_keys_out, void* grads_out, int64_t* num_unique_out,
+                                      void* workspace, uint64_t workspace_bytes, void* stream) {
+  C_TRY
+  NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
+  NVE_CHECK_ARG(num_unique_out != nullptr, "num_unique_out must not be NULL");
+  const bool concat = pooling_type == NVE_POOL_CONCATENATE;
+  int64_t bags = 0;
+  if (!concat) {
+    if (sparse_type == NVE_SPARSE_CSR) {
+      NVE_CHECK_ARG(num_csr_offsets >= 1, "CSR pooling needs num_csr_offsets >= 1");
+      bags = num_csr_offsets - 1;
+    } else {
+      NVE_CHECK_ARG(fixed_hotness > 0 && num_keys % fixed_hotness == 0,
+                    "num_keys must be a multiple of fixed_hotness");
+      bags = num_keys / fixed_hotness;
+    }
+  }
+  *num_unique_out = pooling_backprop_run(key_bytes_of(key_type), num_keys, keys, (int)pooling_type,
+                                         (int)sparse_type, csr_offsets, bags, fixed_hotness, weights,
+                                         dtype_in(weight_type), grads_in, dtype_in(grad_type),
+                                         embedding_width, unique_keys_out, grads_out, workspace,
+                                         workspace_bytes, (hipStream_t)stream);
   return NVE_SUCCESS;
   C_CATCH
 }

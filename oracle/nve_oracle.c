@@ -1107,6 +1107,113 @@ int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, co
 }
 
 /* ------------------------------------------------------------------------- */
+/* training backprop (gradient_calculator.cuh:238-301, dedup_grads_kernel.cuh)*/
+/* ------------------------------------------------------------------------- */
+
+static float load_f(const void* p, int dtype, int64_t i) {
+  return dtype == ORC_F16 ? orc_f16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+
+/* bag holding position p: p / hotness (Fixed), else the b with
+ * offsets[b] <= p < offsets[b+1] found by binary search; -1 for none */
+static int64_t bag_of_pos(int64_t p, int sparse, const void* offsets, int key_bytes,
+                          int64_t num_bags, int64_t hotness) {
+  if (sparse == ORC_FIXED) {
+    const int64_t b = hotness > 0 ? p / hotness : -1;
+    return (b >= 0 && b < num_bags) ? b : -1;
+  }
+  int64_t lo = 0, hi = num_bags; /* largest b in [0, num_bags) with offsets[b] <= p */
+  if (num_bags <= 0 || load_key(offsets, key_bytes, 0) > p) return -1;
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) / 2;
+    if (load_key(offsets, key_bytes, mid) <= p) lo = mid; else hi = mid;
+  }
+  return p < load_key(offsets, key_bytes, lo + 1) ? lo : -1;
+}
+
+int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int pooling, int sparse,
+                             const void* offsets, int64_t num_bags, int64_t hotness,
+                             const void* weights, int weight_dtype, const void* grads_in,
+                             int grad_dtype, int64_t dim, int64_t max_run, void* unique_out,
+                             void* grads_out) {
+  if (n <= 0) return 0;
+  int64_t* uq = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  int64_t* ct = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  int64_t* inv = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  int64_t* off = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+  const int64_t u = orc_dedup(keys, key_bytes, n, uq, ct, inv, off);
+  const int concat = pooling == ORC_CONCAT;
+  const int weighted = pooling == ORC_WSUM || pooling == ORC_WMEAN;
+  const int normalized = pooling == ORC_MEAN || pooling == ORC_WMEAN;
+  float* denom = NULL;
+  if (!concat && normalized) {
+    denom = (float*)calloc((size_t)(num_bags > 0 ? num_bags : 1), sizeof(float));
+    for (int64_t b = 0; b < num_bags; b++) {
+      int64_t s, e;
+      if (sparse == ORC_FIXED) {
+        s = b * hotness;
+        e = s + hotness;
+      } else {
+        s = load_key(offsets, key_bytes, b);
+        e = load_key(offsets, key_bytes, b + 1);
+      }
+      if (pooling == ORC_MEAN) {
+        denom[b] = (float)(e - s);
+      } else {
+        float acc = 0.0f;
+        for (int64_t p = s; p < e; p++) acc += load_f(weights, weight_dtype, p);
+        denom[b] = acc;
+      }
+    }
+  }
+  float* part = (float*)malloc(sizeof(float) * (size_t)dim);
+  float* tot = (float*)malloc(sizeof(float) * (size_t)dim);
+  for (int64_t k = 0; k < u; k++) {
+    for (int64_t c = 0; c < dim; c++) tot[c] = 0.0f;
+    for (int64_t r0 = 0; r0 < ct[k]; r0 += max_run) {
+      const int64_t r1 = (r0 + max_run < ct[k]) ? r0 + max_run : ct[k];
+      for (int64_t c = 0; c < dim; c++) part[c] = 0.0f;
+      for (int64_t j = r0; j < r1; j++) {
+        const int64_t p = inv[off[k] + j];
+        int64_t row;
+        float w = 1.0f;
+        if (concat) {
+          row = p;
+        } else {
+          row = bag_of_pos(p, sparse, offsets, key_bytes, num_bags, hotness);
+          if (row < 0) continue; /* a position in no bag adds nothing */
+          if (weighted) w = load_f(weights, weight_dtype, p);
+          if (normalized) w = (pooling == ORC_MEAN ? 1.0f : w) / denom[row];
+        }
+        for (int64_t c = 0; c < dim; c++) {
+          const float g = load_f(grads_in, grad_dtype, row * dim + c);
+          part[c] = (concat || pooling == ORC_SUM) ? part[c] + g : fmaf(g, w, part[c]);
+        }
+      }
+      for (int64_t c = 0; c < dim; c++) tot[c] = tot[c] + part[c];
+    }
+    for (int64_t c = 0; c < dim; c++) {
+      if (grad_dtype == ORC_F16)
+        ((uint16_t*)grads_out)[k * dim + c] = orc_f32_to_f16(tot[c]);
+      else
+        ((float*)grads_out)[k * dim + c] = tot[c];
+    }
+    if (key_bytes == 4)
+      ((int32_t*)unique_out)[k] = (int32_t)uq[k];
+    else
+      ((int64_t*)unique_out)[k] = uq[k];
+  }
+  free(tot);
+  free(part);
+  free(denom);
+  free(off);
+  free(inv);
+  free(ct);
+  free(uq);
+  return u;
+}
+
+/* ------------------------------------------------------------------------- */
 /* dedup (deduper.cuh:136-221)                                               */
 /* ------------------------------------------------------------------------- */
 

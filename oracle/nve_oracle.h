@@ -33,6 +33,9 @@
  *                                        decay closed form, stale counters
  *                                        after erase, truncation)
  *   orc_dedup                            sorted/unique/inverse round trip
+ *   orc_pooling_backprop                 torch autograd of embedding_bag /
+ *                                        embedding in float64; dyadic Sum exact;
+ *                                        run-length invariance
  * Parity unpinned: orc_cache_insert's decay factor is defined here as
  * (float)pow((double)rate, (double)delta); the reference uses CUDA __powf,
  * whose bits are not published.
@@ -206,6 +209,30 @@ int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* p
 int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
                                    const uint8_t* values, int64_t value_stride,
                                    int64_t max_modify_size);
+
+/* ---- training backprop (GradientCalculator::compute_gradients,
+ * gradient_calculator.cuh:238-301; GradientDedup, dedup_grads_kernel.cuh:57-107) ----
+ * Sparse gradient of a lookup: unique keys ascending (unique_out, key type) and
+ * one gradient row per unique key (grads_out, dim values of grad_dtype F32/F16).
+ *   pooled (pooling Sum/Mean/WSum/WMean): grads_in has one row per bag;
+ *     grad(u) = sum over the positions p of key u of nw(p) * grads_in[bag(p)],
+ *     nw = 1 (Sum), w[p] (WSum), 1/count(bag) (Mean), w[p] / (the bag's weights
+ *     added in position order) (WMean); bag(p) = p / hotness (Fixed) or the bag
+ *     whose [offsets[b], offsets[b+1]) holds p (CSR); a position in no bag adds
+ *     nothing;
+ *   Concatenate: grads_in has one row per key position; grad(u) = sum of the
+ *     rows of u's positions.
+ * Order (defined here; the reference cuts runs at 1024 positions and adds the
+ * pieces with atomics, so its order is not fixed): u's positions, ascending,
+ * are cut into runs of max_run; a run is accumulated in fp32 in position order
+ * (fmaf(g, nw, acc), or acc + g when unweighted: Sum, Concatenate), the runs'
+ * fp32 partial rows are added in run order starting from 0, and the sum is
+ * rounded once to grad_dtype.  Returns the number of unique keys. */
+int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int pooling, int sparse,
+                             const void* offsets, int64_t num_bags, int64_t hotness,
+                             const void* weights, int weight_dtype, const void* grads_in,
+                             int grad_dtype, int64_t dim, int64_t max_run, void* unique_out,
+                             void* grads_out);
 
 /* ---- dedup (deduper.cuh:136-221) ----
  * unique: ascending unique keys; counts; inverse: positions sorted stably by key

@@ -88,6 +88,8 @@ def _declare(L):
     L.orc_histogram_host.argtypes = [P, I32, I64, P, P, P]
     L.orc_cache_insert_host.restype = I64
     L.orc_cache_insert_host.argtypes = [ctypes.POINTER(OrcCache), P, P, P, I64, I64, P, P]
+    L.orc_pooling_backprop.restype = I64
+    L.orc_pooling_backprop.argtypes = [P, I32, I64, I32, I32, P, I64, I64, P, I32, P, I32, I64, I64, P, P]
     L.orc_cache_insert_keys_host.restype = I64
     L.orc_cache_insert_keys_host.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, P, I64, I64]
     L.orc_cache_set.restype = ctypes.c_uint32
@@ -377,3 +379,22 @@ def power_law(x, min_v, max_v, alpha):
     out = np.empty(x.size, np.int64)
     lib().orc_power_law(_p(x), x.size, float(min_v), float(max_v), float(alpha), _p(out))
     return out
+
+
+def pooling_backprop(keys, pooling, sparse, offsets, num_bags, hotness, weights, weight_dtype,
+                     grads_in, grad_dtype, dim, max_run=64):
+    """Sparse gradient (unique keys ascending, rows of grad_dtype bits) of a
+    lookup, in the run order documented in nve_oracle.h."""
+    keys = np.ascontiguousarray(keys)
+    n = keys.size
+    if offsets is not None:
+        offsets = np.ascontiguousarray(offsets, keys.dtype)
+    if weights is not None:
+        weights = np.ascontiguousarray(weights)
+    grads_in = np.ascontiguousarray(grads_in)
+    uq = np.zeros(max(n, 1), keys.dtype)
+    out = np.zeros((max(n, 1), dim), np.uint16 if grad_dtype == F16 else np.float32)
+    u = lib().orc_pooling_backprop(_p(keys), keys.itemsize, n, pooling, sparse, _p(offsets), num_bags,
+                                   hotness, _p(weights), weight_dtype, _p(grads_in), grad_dtype, dim,
+                                   max_run, _p(uq), _p(out))
+    return uq[:u], out[:u]

@@ -65,7 +65,8 @@ def test_insert_from_uvm_erase_clear_sequence():
         assert_same_state(ct)
     resident = [k for k in range(10000) if ct.model.find_way(k) >= 0]
     erase = np.array(resident[:40], np.int64)
-    _lib.call("nve_table_erase", ct.table, ct.ctx, erase.size, vp(to_dev(erase)))
+    d_erase = to_dev(erase)
+    _lib.call("nve_table_erase", ct.table, ct.ctx, erase.size, vp(d_erase))
     assert ct.model.erase(erase) == 40
     assert_same_state(ct)
     for step in range(3):
@@ -124,7 +125,8 @@ def test_lookups_through_host_policy_cache():
     assert_same_state(ct)
     q = rng.integers(0, rows, size=5000).astype(np.int64)
     out = torch.zeros((q.size, ct.width), dtype=torch.uint8, device="cuda")
-    _lib.call("nve_table_find", ct.table, ct.ctx, q.size, vp(to_dev(q)), None, ct.width, vp(out), None)
+    d_q = to_dev(q)
+    _lib.call("nve_table_find", ct.table, ct.ctx, q.size, vp(d_q), None, ct.width, vp(out), None)
     torch.cuda.synchronize()
     rows_ptr, _, misses = ct.model.resolve(q, ct.uvm_np.reshape(-1))
     ref = np.stack([np.frombuffer(ctypes.string_at(int(p), ct.width), np.uint8) for p in rows_ptr])
