@@ -15,8 +15,7 @@ accessed-by the GPUs, memblock.cpp:111-134) is pinned host memory here: with
 XNACK off, that is the memory the MI355X reads over the host link without
 page faults, which is what the reference's advice arranges.
 
-Out of this build (raise NotImplementedInBuild): the training calls
-(`concat_backprop`, `pooling_backprop`), `update` / `accumulate` on GPU tables,
+Out of this build (raise NotImplementedInBuild): `update` / `accumulate` on GPU tables,
 HostEmbedding / HierarchicalEmbedding layers, the parameter-server tables and
 the multi-process memory blocks (NVL / MPI / Dist*).
 """
@@ -323,11 +322,49 @@ class NVEmbedBinding:
         _lib.call("nve_layer_erase", self._layer, self._ctx(stream), int(num_keys),
                   ctypes.c_void_p(keys), int(table_id))
 
-    def concat_backprop(self, *args):
-        _not_in_build("Gradient computation (concat_backprop)")
+    def _backprop(self, what, num_keys, keys, grads, unique_keys, output_grads, pooling_type,
+                  num_bags, offsets, weight_type, weights, stream):
+        if self.device_id_ < 0:
+            raise _lib.InvalidArgument(
+                _lib.INVALID_ARGUMENT,
+                f"{what} is not supported on a host-only layer (device_id < 0). "
+                "Gradient computation requires a GPU device; HostLayer is inference-only.")
+        import torch
+        dim = self.get_embedding_dim()
+        need = ctypes.c_uint64()
+        _lib.call("nve_amd_backprop_workspace_size", int(num_keys), int(num_bags), dim, ctypes.byref(need))
+        ws = getattr(self, "_bp_ws", None)
+        if ws is None or ws.numel() < need.value:
+            ws = self._bp_ws = torch.empty(max(int(need.value), 1), dtype=torch.uint8,
+                                           device=f"cuda:{self.device_id_}")
+        nu = ctypes.c_int64()
+        _lib.call("nve_amd_pooling_backprop", _lib.KEY_INT64, int(num_keys), ctypes.c_void_p(keys),
+                  int(pooling_type), _lib.SPARSE_CSR, ctypes.c_void_p(offsets),
+                  int(num_bags) + 1 if offsets else 0, 0, ctypes.c_void_p(weights), int(weight_type),
+                  ctypes.c_void_p(grads), int(self.data_type_), dim, ctypes.c_void_p(unique_keys),
+                  ctypes.c_void_p(output_grads), ctypes.byref(nu), ctypes.c_void_p(ws.data_ptr()),
+                  need.value, ctypes.c_void_p(int(stream or 0)))
+        return nu.value
 
-    def pooling_backprop(self, *args):
-        _not_in_build("Gradient computation (pooling_backprop)")
+    def concat_backprop(self, num_keys, keys, grads, unique_keys, output_grads, stream):
+        """Sparse gradient of a per-key lookup (binding_layers.hpp:131-189): the
+        unique keys ascending into unique_keys and, per unique key, the sum of
+        the gradient rows of its positions into output_grads (the table's
+        dtype); returns the number of unique keys."""
+        return self._backprop("concat_backprop", num_keys, keys, grads, unique_keys, output_grads,
+                              PoolingType_t.Concatenate, 0, 0, DataType_t.Unknown, 0, stream)
+
+    def pooling_backprop(self, num_keys, keys, grads, unique_keys, output_grads, pooling_type,
+                         num_offsets, offsets, data_type, weights, stream):
+        """Sparse gradient of a CSR-pooled lookup (binding_layers.hpp:191-250):
+        grads holds one row per bag (num_offsets bags, offsets of num_offsets + 1
+        int64 entries); weights (weighted modes) are per key, of data_type or,
+        when that is not a float type, of the table's dtype."""
+        wt = DataType_t(data_type) if int(data_type) in (int(DataType_t.Float32),
+                                                          int(DataType_t.Float16)) else self.data_type_
+        return self._backprop("pooling_backprop", num_keys, keys, grads, unique_keys, output_grads,
+                              pooling_type, num_offsets, offsets, wt if weights else DataType_t.Unknown,
+                              weights, stream)
 
     def get_num_tables(self):
         out = ctypes.c_int64()

@@ -230,17 +230,93 @@ def test_uvm_insert_erase_clear():
     assert torch.equal(layer(keys), torch.zeros(5, 2, device="cuda"))
 
 
-def test_backward_is_not_in_this_build():
+def _coalesced(grad):
+    g = grad.coalesce()
+    return g.indices().cpu(), g.values().float().cpu()
+
+
+@pytest.mark.parametrize("layer_type", [LT.GPULayer, LT.LinearUVM], ids=["gpu", "uvm"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_embedding_backward_matches_torch(layer_type, dtype):
+    # NVEmbeddingOpTraining.backward (nve_ops.py:108-127): the sparse table
+    # gradient equals torch.nn.Embedding(sparse=True)'s; 2-D keys with repeats
+    # (the op returns one row per key, [keys.numel(), dim])
     torch.manual_seed(5)
+    rows, dim = 1000, 16
+    ref = torch.nn.Embedding(rows, dim, sparse=True, device="cuda")
+    layer = make(layer_type, ref.weight.detach().to(dtype), train=True)
+    keys = torch.randint(0, 200, (64, 5), device="cuda")
+    g_out = torch.randn(64 * 5, dim, device="cuda").to(dtype)
+    (layer(keys) * g_out).sum().backward()
+    (ref(keys).reshape(-1, dim) * g_out.float()).sum().backward()
+    gi, gv = _coalesced(layer.weight.grad)
+    ri, rv = _coalesced(ref.weight.grad)
+    assert torch.equal(gi, ri)
+    tol = 1e-5 if dtype == torch.float32 else 2.0 ** -10  # fp16: one rounding of an fp32 sum
+    assert torch.allclose(gv, rv, rtol=tol, atol=tol * rv.abs().max().item())
+    assert layer.weight.grad.dtype == dtype
+
+
+@pytest.mark.parametrize("mode,weighted", [("sum", False), ("mean", False), ("sum", True)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_embedding_bag_backward_matches_torch(mode, weighted, dtype):
+    # NVEmbeddingBagOpTraining.backward (nve_ops.py:186-226) against
+    # torch.nn.EmbeddingBag(sparse=True, include_last_offset=True), empty bags included
+    torch.manual_seed(7)
+    rows, dim, bags = 5000, 32, 300
+    ref = torch.nn.EmbeddingBag(rows, dim, mode=mode, sparse=True, include_last_offset=True, device="cuda")
+    layer = make(LT.GPULayer, ref.weight.detach().to(dtype), bag_mode=mode, train=True)
+    lens = torch.randint(0, 40, (bags,))
+    lens[::11] = 0
+    offsets = torch.zeros(bags + 1, dtype=torch.int64)
+    offsets[1:] = torch.cumsum(lens, 0)
+    n = int(offsets[-1])
+    keys = (torch.from_numpy(np.random.default_rng(3).zipf(1.2, size=n)) % rows).to(torch.int64).cuda()
+    offsets = offsets.cuda()
+    psw = torch.rand(n, device="cuda").to(dtype) if weighted else None
+    g_out = torch.randn(bags, dim, device="cuda").to(dtype)
+    (layer(keys, offsets, psw) * g_out).sum().backward()
+    (ref(keys, offsets, per_sample_weights=None if psw is None else psw.float()) * g_out.float()).sum().backward()
+    gi, gv = _coalesced(layer.weight.grad)
+    ri, rv = _coalesced(ref.weight.grad)
+    assert torch.equal(gi, ri)
+    tol = 1e-5 if dtype == torch.float32 else 2.0 ** -10
+    assert torch.allclose(gv, rv, rtol=tol, atol=tol * rv.abs().max().item())
+
+
+def test_sgd_steps_match_torch_embedding_bag():
+    # a sparse-gradient training loop: SGD applies the gradient through
+    # CachedTable.add_ (nve_tensors.py:64-80) into the layer's table
+    torch.manual_seed(11)
+    rows, dim, bags, hot = 2000, 16, 64, 8
+    ref = torch.nn.EmbeddingBag(rows, dim, mode="sum", sparse=True, include_last_offset=True, device="cuda")
+    layer = make(LT.GPULayer, ref.weight.detach().clone(), bag_mode="sum", train=True)
+    opt_ref = torch.optim.SGD(ref.parameters(), lr=0.05, foreach=False)
+    opt = torch.optim.SGD([layer.weight], lr=0.05, foreach=False)
+    offsets = torch.arange(0, bags * hot + 1, hot, device="cuda")
+    for step in range(4):
+        keys = torch.randint(0, 300, (bags * hot,), device="cuda")
+        target = torch.randn(bags, dim, device="cuda")
+        for model, o in ((layer, opt), (ref, opt_ref)):
+            o.zero_grad()
+            ((model(keys, offsets) - target) ** 2).sum().backward()
+            o.step()
+    torch.cuda.synchronize()
+    probe = torch.arange(0, 300, device="cuda")
+    one = torch.arange(0, 301, device="cuda")
+    with torch.no_grad():
+        assert torch.allclose(layer(probe, one), ref(probe, one), rtol=1e-5, atol=1e-5)
+
+
+def test_inference_layer_has_no_gradient_path():
+    # optimize_for_training=False: the op does not take the weight, so the
+    # output is not part of an autograd graph (nve_ops.py:65-86)
     w = torch.randn(100, 4)
     keys = torch.tensor([1, 2, 3], dtype=torch.int64, device="cuda")
-    train = make(LT.GPULayer, w, train=True)
-    out = train(keys)
-    assert out.requires_grad
-    with pytest.raises(NotImplementedError, match="not part of this build"):
-        out.sum().backward()
     infer = make(LT.GPULayer, w, train=False)
-    assert torch.equal(infer(keys), w[keys.cpu()].cuda())
+    out = infer(keys)
+    assert not out.requires_grad
+    assert torch.equal(out, w[keys.cpu()].cuda())
 
 
 @pytest.mark.parametrize("layer_type", [LT.GPULayer, LT.LinearUVM], ids=["gpu", "uvm"])
