@@ -175,7 +175,8 @@ def quant_rows_e4m3(torch, n, gen):
 def run_workload(args, torch, _lib):
     """Parity-test configurations of BASELINE.json measured the same way
     (not the contract line): c2 (dedup then gather), c4a / c4b (dequant),
-    c5 (26-table jagged weighted mean)."""
+    c5 (26-table jagged weighted mean), c3 (LinearUVM cache over a host
+    table) and c2bwd (training backprop of the c2pool lookup)."""
     L = _lib.load()
     stream = torch.cuda.Stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
@@ -352,6 +353,45 @@ def run_workload(args, torch, _lib):
         hip.hipHostFree(host_ptr)
         kernel = ("gather_kernel / SortGather / PipelineGather (cache + host misses)" if concat
                   else "pool_kernel (cache + host misses)")
+    elif w == "c2bwd":
+        # training backprop of the headline lookup: the sparse table gradient of
+        # 256 bags x 1024 Zipf(1.05) keys (50M-row range) from a 256 x 128 fp16
+        # output gradient (dedup, rows and weights per position, run pooling)
+        rows, dim, bags, hot, alpha = 50_000_000, 128, 256, 1024, 1.05
+        nkeys = bags * hot
+        pg = torch.Generator(device="cuda")
+        pg.manual_seed(31337)
+        perm = torch.randperm(rows, generator=pg, device="cuda", dtype=torch.int64)
+        batches = [power_law_keys(torch, nkeys, rows, alpha, kgen, perm) for _ in range(args.batches)]
+        del perm
+        gg = torch.Generator(device="cuda")
+        gg.manual_seed(5)
+        grads = torch.randn((bags, dim), device="cuda", generator=gg).to(torch.float16)
+        uq = torch.empty(nkeys, dtype=torch.int64, device="cuda")
+        gout = torch.empty((nkeys, dim), dtype=torch.float16, device="cuda")
+        wsb = ctypes.c_uint64()
+        _lib.call("nve_amd_backprop_workspace_size", nkeys, bags, dim, ctypes.byref(wsb))
+        ws = torch.empty(int(wsb.value), dtype=torch.uint8, device="cuda")
+        nu = ctypes.c_int64()
+        kp = [ctypes.c_void_p(b.data_ptr()) for b in batches]
+        uniq = []
+
+        def step(i):
+            _lib.check(L.nve_amd_pooling_backprop(
+                _lib.KEY_INT64, nkeys, kp[i % len(kp)], _lib.POOL_SUM, _lib.SPARSE_FIXED, None, 0, hot, None,
+                _lib.DT_UNKNOWN, ctypes.c_void_p(grads.data_ptr()), _lib.DT_F16, dim,
+                ctypes.c_void_p(uq.data_ptr()), ctypes.c_void_p(gout.data_ptr()), ctypes.byref(nu),
+                ctypes.c_void_p(ws.data_ptr()), wsb.value, sp))
+            uniq.append(nu.value)
+
+        ms = time_steps(torch, stream, step, args.warmup, args.steps)
+        u = sum(uniq) // len(uniq)
+        # keys + one gradient row read per key position + unique keys and rows written
+        alg = nkeys * 8 + nkeys * dim * 2 + u * (8 + dim * 2)
+        cfg_out.update({"table_rows": rows, "dim": dim, "bags": bags, "hotness": hot, "zipf_alpha": alpha,
+                        "keys_per_batch": nkeys, "mean_unique_keys": u, "pooling": "sum",
+                        "grad_dtype": "f16", "step": "one nve_amd_pooling_backprop call (synchronizes)"})
+        kernel = "dedup sort + backprop_prep + pool_kernel (runs, then per key)"
     elif w == "c5":
         T, B, dim = 26, 8192, 128
         cg = torch.Generator()
@@ -416,7 +456,8 @@ def run_workload(args, torch, _lib):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="c2pool", choices=["c2pool", "c2", "c3", "c4a", "c4b", "c5"],
+    ap.add_argument("--workload", default="c2pool",
+                    choices=["c2pool", "c2", "c2bwd", "c3", "c4a", "c4b", "c5"],
                     help="c2pool (default, the metric's configuration) or a parity configuration")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)

@@ -127,11 +127,8 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
   void* scan_tmp = b.dedup_ws + 256;
   NVE_HIP(launch_run_count(b.counts, key_bytes, u, kMaxRun, b.nruns, s));
   NVE_HIP(exclusive_scan_u32(b.nruns, u, total, scan_tmp, s));
-  uint32_t runs = 0;
-  NVE_HIP(hipMemcpyAsync(&runs, total, sizeof(runs), hipMemcpyDeviceToHost, s));
-  NVE_HIP(hipStreamSynchronize(s));
-  NVE_HIP(launch_run_write(b.doff, b.counts, key_bytes, u, n, kMaxRun, b.nruns, runs, b.run_off,
-                           b.key_run_off, s));
+  const uint32_t runs = read_back(total, s);
+  NVE_HIP(launch_run_write(b.doff, key_bytes, u, n, kMaxRun, b.nruns, runs, b.run_off, b.key_run_off, s));
 
   const int ges = gdt == kF16 ? 2 : 4;
   // (4) one fp32 partial row per run, positions in order

@@ -69,9 +69,7 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, s));
   NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(b.span), 1, 0, s));
   NVE_HIP(key_span(b.ka, n, b.span, s));
-  unsigned long long span = 0;
-  NVE_HIP(hipMemcpyAsync(&span, b.span, sizeof(span), hipMemcpyDeviceToHost, s));
-  NVE_HIP(hipStreamSynchronize(s));
+  const unsigned long long span = read_back(b.span, s);
   int alt = 0;
   NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, (bits_for(span) + 7) / 8 * 8, b.sort_tmp,
                            &alt, s));
@@ -80,9 +78,7 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   NVE_HIP(launch_run_heads(ks, n, b.heads, s));
   NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, b.sort_tmp, s));
   NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, s));
-  uint32_t u = 0;
-  NVE_HIP(hipMemcpyAsync(&u, b.total, sizeof(u), hipMemcpyDeviceToHost, s));
-  NVE_HIP(hipStreamSynchronize(s));
+  const uint32_t u = read_back(b.total, s);
   NVE_HIP(launch_dedup_counts(b.start, u, key_bytes, counts, s));
   return (int64_t)u;
 }

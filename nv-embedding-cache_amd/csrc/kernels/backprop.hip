@@ -97,20 +97,25 @@ __global__ __launch_bounds__(256) void run_count_kernel(const void* counts, int 
 }
 
 // run_off: run r covers dedup positions [run_off[r], run_off[r + 1]);
-// key_run_off: key k owns runs [key_run_off[k], key_run_off[k + 1]).
-__global__ __launch_bounds__(256) void run_write_kernel(const void* doff, const void* counts,
-                                                        int key_bytes, int64_t u, int64_t n,
-                                                        int64_t max_run, const uint32_t* run_scan,
-                                                        uint32_t total, void* run_off,
-                                                        void* key_run_off) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= u) return;
-  const int64_t base = run_scan[k];
-  const int64_t s = load_key(doff, key_bytes, k);
-  const int64_t c = load_key(counts, key_bytes, k);
-  for (int64_t i = 0; i * max_run < c; ++i) store_key(run_off, key_bytes, base + i, s + i * max_run);
-  store_key(key_run_off, key_bytes, k, base);
-  if (k == u - 1) {
+// key_run_off: key k owns runs [key_run_off[k], key_run_off[k + 1]).  One
+// thread per run (its key found by binary search in the exclusive scan of
+// the run counts, every key owning at least one run) and per key.
+__global__ __launch_bounds__(256) void run_write_kernel(const void* doff, int key_bytes, int64_t u,
+                                                        int64_t n, int64_t max_run,
+                                                        const uint32_t* run_scan, uint32_t total,
+                                                        void* run_off, void* key_run_off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (int64_t)total) {
+    int64_t lo = 0, hi = u;  // last k with run_scan[k] <= i
+    while (hi - lo > 1) {
+      const int64_t mid = (lo + hi) >> 1;
+      if ((int64_t)run_scan[mid] <= i) lo = mid;
+      else hi = mid;
+    }
+    store_key(run_off, key_bytes, i, load_key(doff, key_bytes, lo) + (i - (int64_t)run_scan[lo]) * max_run);
+  }
+  if (i < u) store_key(key_run_off, key_bytes, i, run_scan[i]);
+  if (i == 0) {
     store_key(run_off, key_bytes, total, n);
     store_key(key_run_off, key_bytes, u, total);
   }
@@ -146,12 +151,13 @@ hipError_t launch_run_count(const void* counts, int key_bytes, int64_t u, int64_
   return hipGetLastError();
 }
 
-hipError_t launch_run_write(const void* doff, const void* counts, int key_bytes, int64_t u, int64_t n,
-                            int64_t max_run, const uint32_t* run_scan, uint32_t total, void* run_off,
-                            void* key_run_off, hipStream_t stream) {
+hipError_t launch_run_write(const void* doff, int key_bytes, int64_t u, int64_t n, int64_t max_run,
+                            const uint32_t* run_scan, uint32_t total, void* run_off, void* key_run_off,
+                            hipStream_t stream) {
   if (u <= 0) return hipSuccess;
-  hipLaunchKernelGGL(run_write_kernel, dim3((unsigned)((u + 255) / 256)), dim3(256), 0, stream, doff,
-                     counts, key_bytes, u, n, max_run, run_scan, total, run_off, key_run_off);
+  const int64_t m = (int64_t)total > u ? (int64_t)total : u;
+  hipLaunchKernelGGL(run_write_kernel, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, stream, doff,
+                     key_bytes, u, n, max_run, run_scan, total, run_off, key_run_off);
   return hipGetLastError();
 }
 

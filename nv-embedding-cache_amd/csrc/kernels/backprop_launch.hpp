@@ -18,8 +18,8 @@ hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, i
                                 void* rowkey, float* nw, hipStream_t stream);
 hipError_t launch_run_count(const void* counts, int key_bytes, int64_t u, int64_t max_run,
                             uint32_t* nruns, hipStream_t stream);
-hipError_t launch_run_write(const void* doff, const void* counts, int key_bytes, int64_t u, int64_t n,
-                            int64_t max_run, const uint32_t* run_scan, uint32_t total, void* run_off,
-                            void* key_run_off, hipStream_t stream);
+hipError_t launch_run_write(const void* doff, int key_bytes, int64_t u, int64_t n, int64_t max_run,
+                            const uint32_t* run_scan, uint32_t total, void* run_off, void* key_run_off,
+                            hipStream_t stream);
 
 }  // namespace nve_amd

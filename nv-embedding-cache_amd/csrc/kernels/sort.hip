@@ -244,9 +244,12 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
   }
 }
 
-// OR over i of keys[i] ^ keys[0]: the bits where keys differ.
+// OR over i of keys[i] ^ keys[0]: the bits where keys differ.  One atomic per
+// workgroup at most, and none when the workgroup adds no new bit: thousands
+// of atomics on one address serialize in one L2 channel.
 __global__ __launch_bounds__(256) void key_span_kernel(const uint64_t* keys, int64_t n,
                                                        unsigned long long* out) {
+  __shared__ uint64_t red[4];
   const uint64_t k0 = keys[0];
   uint64_t acc = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -254,7 +257,13 @@ __global__ __launch_bounds__(256) void key_span_kernel(const uint64_t* keys, int
     acc |= keys[i] ^ k0;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) acc |= __shfl_xor(acc, o);
-  if ((threadIdx.x & 63) == 0 && acc) atomicOr(out, (unsigned long long)acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint64_t a = red[0] | red[1] | red[2] | red[3];
+    const uint64_t seen = __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a & ~seen) atomicOr(out, (unsigned long long)a);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -323,8 +332,8 @@ hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, void* 
 
 hipError_t key_span(const uint64_t* keys, int64_t n, unsigned long long* out, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
-  int64_t grid = (n + 255) / 256;
-  if (grid > 1024) grid = 1024;
+  int64_t grid = (n + 1023) / 1024;  // four keys per thread
+  if (grid > 512) grid = 512;
   hipLaunchKernelGGL(key_span_kernel, dim3(grid), dim3(256), 0, stream, keys, n, out);
   return hipGetLastError();
 }

@@ -43,10 +43,7 @@ T* carve(uint8_t*& p, size_t count) {
 }
 
 uint32_t read_u32(const uint32_t* d, hipStream_t s) {
-  uint32_t h = 0;
-  NVE_HIP(hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, s));
-  NVE_HIP(hipStreamSynchronize(s));
-  return h;
+  return read_back(d, s);
 }
 
 }  // namespace
@@ -134,9 +131,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   NVE_HIP(launch_hist_prep(d_keys, key_bytes_, n, ka, va, s));
   NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(d_span), 1, 0, s));
   NVE_HIP(key_span(ka, n, d_span, s));
-  unsigned long long span = 0;
-  NVE_HIP(hipMemcpyAsync(&span, d_span, sizeof(span), hipMemcpyDeviceToHost, s));
-  NVE_HIP(hipStreamSynchronize(s));
+  const unsigned long long span = read_back(d_span, s);
   int alt = 0;
   NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, round8(bits_for(span)), sort_tmp, &alt, s));
   uint64_t* ks = alt ? kb : ka;

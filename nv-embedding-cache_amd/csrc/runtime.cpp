@@ -9,6 +9,16 @@
 
 namespace nve_amd {
 
+void read_small(void* host, const void* dev, size_t bytes, hipStream_t stream) {
+  NVE_CHECK(bytes <= 64, "read_small reads at most 64 bytes");
+  // one pinned slot per thread, kept for the thread's life
+  thread_local void* slot = nullptr;
+  if (slot == nullptr) NVE_HIP(hipHostMalloc(&slot, 64, hipHostMallocDefault));
+  NVE_HIP(hipMemcpyAsync(slot, dev, bytes, hipMemcpyDeviceToHost, stream));
+  NVE_HIP(hipStreamSynchronize(stream));
+  std::memcpy(host, slot, bytes);
+}
+
 ScopedDevice::ScopedDevice(int device) {
   if (device < 0) return;
   NVE_HIP(hipGetDevice(&prev_));
@@ -192,10 +202,7 @@ void ExecutionContext::reset_misses() {
 }
 
 int64_t ExecutionContext::read_misses() {
-  unsigned long long h = 0;
-  NVE_HIP(hipMemcpyAsync(&h, miss_counter(), sizeof(h), hipMemcpyDeviceToHost, lookup_));
-  NVE_HIP(hipStreamSynchronize(lookup_));
-  return (int64_t)h;
+  return (int64_t)read_back(miss_counter(), lookup_);
 }
 
 void ExecutionContext::add_pending(std::future<void> f) {

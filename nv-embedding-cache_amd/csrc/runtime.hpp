@@ -177,6 +177,17 @@ const void* device_input(ExecutionContext& ctx, const char* name, const void* p,
 const void* host_input(ExecutionContext& ctx, const char* name, const void* p, size_t bytes,
                        hipStream_t stream);
 
+// Copies `bytes` (at most 64) of device memory to `host` and waits for
+// `stream`.  The copy lands in a pinned per-thread slot first: a pageable
+// destination costs a staged copy, tens of microseconds for a few bytes.
+void read_small(void* host, const void* dev, size_t bytes, hipStream_t stream);
+template <typename T>
+T read_back(const T* dev, hipStream_t stream) {
+  T h;
+  read_small(&h, dev, sizeof(T), stream);
+  return h;
+}
+
 // fp16 <-> fp32 on the host (round to nearest even; NaN stays NaN).
 float half_bits_to_float(uint16_t h);
 uint16_t float_to_half_bits(float f);

@@ -75,10 +75,7 @@ SortedLookups sort_lookups(ExecutionContext& ctx, const GatherLaunch& g, int key
   NVE_HIP(launch_permute_keys(g.keys, key_bytes, pos, n, sorted_keys, s));
   SortedLookups r{pos, sorted_keys, 0};
   if (want_misses) {
-    unsigned long long m = 0;
-    NVE_HIP(hipMemcpyAsync(&m, nmiss, sizeof(m), hipMemcpyDeviceToHost, s));
-    NVE_HIP(hipStreamSynchronize(s));
-    r.misses = (uint32_t)m;
+    r.misses = (uint32_t)read_back(nmiss, s);
   }
   return r;
 }
