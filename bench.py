@@ -427,10 +427,11 @@ def run_workload(args, torch, _lib):
         nkeys = sum(s[0].numel() for s in sets) // len(sets)
         out = torch.empty((B, T, dim), dtype=torch.float32, device="cuda")
         ptrs = (ctypes.c_void_p * T)(*[t.data_ptr() for t in tables])
+        rows_arr = (ctypes.c_int64 * T)(*cards)
 
         def step(i):
             keys, off, wts = sets[i % len(sets)]
-            _lib.call("nve_amd_find_and_pool_multi", _lib.KEY_INT64, T, ptrs, dim * 2, _lib.DT_F16, B,
+            _lib.call("nve_amd_find_and_pool_multi", _lib.KEY_INT64, T, ptrs, rows_arr, dim * 2, _lib.DT_F16, B,
                       keys.numel(), ctypes.c_void_p(keys.data_ptr()), ctypes.c_void_p(off.data_ptr()),
                       ctypes.c_void_p(wts.data_ptr()), _lib.DT_F32, _lib.POOL_WMEAN, _lib.DT_F32,
                       ctypes.c_void_p(out.data_ptr()), sp)

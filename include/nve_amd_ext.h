@@ -49,7 +49,9 @@ NVE_C_API nve_status_t nve_amd_find_and_pool(
 /* Multi-table jagged pooling in one launch (the reference pools one table per
  * call; this fuses a batch of num_tables tables of equal row format, as a
  * TorchRec KeyedJaggedTensor lays them out).  tables: host array of
- * num_tables device table pointers.  keys: num_keys keys of the key type,
+ * num_tables device table pointers; table_rows: host array of their row
+ * counts (keys outside [0, table_rows[t]) read nothing), or NULL for no bound
+ * check.  keys: num_keys keys of the key type,
  * table-major.  offsets: num_tables*batch_size + 1 entries of the key type;
  * bag (t, b) holds keys [offsets[t*batch_size + b], offsets[t*batch_size+b+1]).
  * weights: per key (weighted pooling), f32 or f16.  output: batch_size rows of
@@ -58,7 +60,8 @@ NVE_C_API nve_status_t nve_amd_find_and_pool(
  * WeightedMean, fp32 accumulation; an fp16 or fp32 output from any row format. */
 NVE_C_API nve_status_t nve_amd_find_and_pool_multi(
     nve_key_type_t key_type, int64_t num_tables, const void* const* tables,
-    int64_t row_size_in_bytes, nve_data_type_t value_dtype, int64_t batch_size, int64_t num_keys,
+    const int64_t* table_rows, int64_t row_size_in_bytes, nve_data_type_t value_dtype,
+    int64_t batch_size, int64_t num_keys,
     const void* keys, const void* offsets, const void* weights, nve_data_type_t weight_type,
     nve_pooling_type_t pooling_type, nve_data_type_t output_type, void* output, void* stream);
 

@@ -730,7 +730,8 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
 }
 
 nve_status_t nve_amd_find_and_pool_multi(nve_key_type_t key_type, int64_t num_tables,
-                                         const void* const* tables, int64_t row_size_in_bytes,
+                                         const void* const* tables, const int64_t* table_rows,
+                                         int64_t row_size_in_bytes,
                                          nve_data_type_t value_dtype, int64_t batch_size,
                                          int64_t num_keys, const void* keys, const void* offsets,
                                          const void* weights, nve_data_type_t weight_type,
@@ -759,7 +760,10 @@ nve_status_t nve_amd_find_and_pool_multi(nve_key_type_t key_type, int64_t num_ta
   if (is_rowwise(vdt)) NVE_CHECK_ARG(row_size_in_bytes % 2 == 0, "Quantized rows must have an even width");
   const int64_t count = (row_size_in_bytes - meta) / value_elem_bytes(vdt);
   const int64_t oes = dtype_size(odt);
-  for (int64_t t = 0; t < num_tables; ++t) NVE_CHECK_ARG(tables[t] != nullptr, "table ", t, " is NULL");
+  for (int64_t t = 0; t < num_tables; ++t) {
+    NVE_CHECK_ARG(tables[t] != nullptr, "table ", t, " is NULL");
+    if (table_rows) NVE_CHECK_ARG(table_rows[t] > 0, "table ", t, " has no rows");
+  }
   for (int64_t t0 = 0; t0 < num_tables; t0 += kMaxPoolTables) {
     const int64_t nt = std::min<int64_t>(kMaxPoolTables, num_tables - t0);
     PoolLaunch p{};
@@ -786,7 +790,10 @@ nve_status_t nve_amd_find_and_pool_multi(nve_key_type_t key_type, int64_t num_ta
     p.keys_per_bag = std::max<int64_t>(1, num_keys / (num_tables * batch_size));
     p.bags_per_table = batch_size;
     p.out_table_stride = count * oes;
-    for (int64_t t = 0; t < nt; ++t) p.tables[t] = static_cast<const uint8_t*>(tables[t0 + t]);
+    for (int64_t t = 0; t < nt; ++t) {
+      p.tables[t] = static_cast<const uint8_t*>(tables[t0 + t]);
+      p.table_rows[t] = table_rows ? (uint64_t)table_rows[t0 + t] : 0;  // 0: no bound check
+    }
     NVE_HIP(launch_pool(p, (hipStream_t)stream));
   }
   return NVE_SUCCESS;

@@ -74,6 +74,7 @@ struct PoolLaunch {
   int64_t bags_per_table;
   int64_t out_table_stride;
   const uint8_t* tables[kMaxPoolTables];
+  uint64_t table_rows[kMaxPoolTables];  // rows of each table (0: no bound check)
 };
 
 hipError_t launch_gather(const GatherLaunch& a, hipStream_t stream);

@@ -388,6 +388,7 @@ hipError_t launch_pool(const PoolLaunch& a, hipStream_t stream) {
   if (!pool_geometry(a, &g)) return hipErrorInvalidValue;
   if (g.grid > 0x7fffffffLL) return hipErrorInvalidValue;
   if (a.force_unroll == 0 && pool_split_eligible(a, g)) return launch_pool_split(a, g, stream);
+  if (a.force_unroll == 0 && pool_short_eligible(a, g)) return launch_pool_short(a, g, stream);
   switch (a.stored_dtype) {
     case kF32:
     case kF16:

@@ -69,7 +69,10 @@ __global__ __launch_bounds__(1024) void pool_kernel(PoolLaunch a, int g_shift, i
   }
   // the bag's table (several tables in one launch) and output row
   RowSource src = a.src;
-  if (a.num_tables > 0 && live) src.table = a.tables[bag / a.bags_per_table];
+  if (a.num_tables > 0 && live) {
+    src.table = a.tables[bag / a.bags_per_table];
+    src.num_rows = a.table_rows[bag / a.bags_per_table];
+  }
   int64_t cs = s, ce = e;
   if (gpb > 1 && e > s) {
     const int64_t per = (e - s + gpb - 1) >> gpb_shift;

@@ -18,5 +18,9 @@ hipError_t launch_pool_ext(const PoolLaunch& a, const PoolGeometry& g, hipStream
 // as pool_kernel's split-bag path with fewer instructions.
 bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g);
 hipError_t launch_pool_split(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
+// Short bags (one lane group per bag) over linear f16 / f32 tables, one or
+// several (pool_split.hip): the same sums as pool_kernel's one-group path.
+bool pool_short_eligible(const PoolLaunch& a, const PoolGeometry& g);
+hipError_t launch_pool_short(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream);
 
 }  // namespace nve_amd

@@ -1,7 +1,10 @@
-// pool_split.hip -- find-and-pool for long bags over a linear table: the
-// shape of the GPULayer benchmark (a few hundred bags of ~1K keys, rows of
-// 16-byte lane slices), where the general pool_kernel spends most of its time
-// on instructions rather than on memory.
+// pool_split.hip -- find-and-pool over linear tables without the general
+// pool_kernel's generality (cache, backing table, passes, 64-bit address
+// shuffles, a 1 KB argument block):
+//  * pool_split_kernel: long bags (the GPULayer benchmark: a few hundred bags
+//    of ~1K keys), one workgroup per bag;
+//  * pool_short_kernel: short bags (DLRM-style jagged batches, one or many
+//    tables), one lane group per bag.
 //
 // Reference behaviour restated: find_and_combine (cuda_ops/find_and_combine_kernel.cuh:40-154)
 // over a linear table (GPULayer, gpu_embedding_layer.cu:153-189).
@@ -84,6 +87,15 @@ __device__ __forceinline__ void group_bcast_batch(uint32_t ridx, float w, int la
     ri[u] = group_bcast<G, J0 + u>(ridx, lane);
     wu[u] = W ? __uint_as_float(group_bcast<G, J0 + u>(__float_as_uint(w), lane)) : 1.0f;
     group_bcast_batch<G, U, W, J0, u + 1>(ridx, w, lane, ri, wu);
+  }
+}
+
+// f(integral_constant<int, b * U>) for b = B .. NB - 1, unrolled at compile time
+template <int U, int B, int NB, typename F>
+__device__ __forceinline__ void for_batches(F& f) {
+  if constexpr (B < NB) {
+    f(std::integral_constant<int, B * U>{});
+    for_batches<U, B + 1, NB>(f);
   }
 }
 
@@ -207,12 +219,7 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
         }
       }
     };
-    batch(std::integral_constant<int, 0>{});
-    if constexpr (G / U > 1) batch(std::integral_constant<int, U>{});
-    if constexpr (G / U > 2) {
-      batch(std::integral_constant<int, 2 * U>{});
-      batch(std::integral_constant<int, 3 * U>{});
-    }
+    for_batches<U, 0, G / U>(batch);
   }
 
   // butterfly over the wave's groups (the same pairing and additions as pool_kernel)
@@ -298,7 +305,223 @@ hipError_t launch_split_sdt(const PoolLaunch& a, const PoolGeometry& g, hipStrea
   }
 }
 
+// ---------------------------------------------------------------------------
+// short bags: one G-lane group per bag, 256 / G bags per workgroup, the bag's
+// keys in key order (the same additions as pool_kernel's one-group-per-bag
+// path, so the same bits).  MT: several tables in one launch (bag b belongs to
+// table b / bags_per_table and writes row (b % bags_per_table) * out_stride +
+// table * out_table_stride).
+// ---------------------------------------------------------------------------
+struct ShortArgs {
+  const void* keys;
+  const void* offsets;  // null: fixed hotness
+  const void* weights;
+  void* out;
+  const uint8_t* table;  // one table (MT = false)
+  int64_t num_keys;
+  int64_t num_bags;
+  int64_t hotness;
+  uint64_t row_bytes;
+  uint64_t num_rows;
+  int64_t count;
+  int64_t out_stride;
+  int64_t bags_per_table;
+  int64_t out_table_stride;
+  int key_bytes;
+  int weight_dtype;
+  int mean;
+  int out_dtype;
+};
+struct ShortArgsMT : ShortArgs {
+  const uint8_t* tables[kMaxPoolTables];
+  uint32_t table_rows[kMaxPoolTables];
+};
+
+template <int SDT, int G, bool W, bool MT, int UMAX>
+__global__ __launch_bounds__(256) void pool_short_kernel(
+    typename std::conditional<MT, ShortArgsMT, ShortArgs>::type a) {
+  constexpr int VB = 16;
+  constexpr int ES = Fmt<SDT>::esize;
+  constexpr int E = VB / ES;
+  constexpr int U = G < UMAX ? G : UMAX;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int gl = tid & (G - 1);
+  const int64_t bag = (int64_t)blockIdx.x * (256 / G) + tid / G;
+  const bool live = bag < a.num_bags;  // uniform over the group
+
+  int64_t s = 0, e = 0;
+  if (live) {
+    if (a.offsets != nullptr) {
+      s = load_key(a.offsets, a.key_bytes, bag);
+      e = load_key(a.offsets, a.key_bytes, bag + 1);
+      s = s < 0 ? 0 : (s > a.num_keys ? a.num_keys : s);
+      e = e < s ? s : (e > a.num_keys ? a.num_keys : e);
+    } else {
+      s = bag * a.hotness;
+      e = s + a.hotness;
+    }
+  }
+  uint64_t table = (uint64_t)a.table;
+  uint64_t num_rows = a.num_rows;
+  uint8_t* out_row = reinterpret_cast<uint8_t*>(a.out);
+  if constexpr (MT) {
+    const int64_t t = live ? bag / a.bags_per_table : 0;
+    table = (uint64_t)a.tables[t];
+    num_rows = a.table_rows[t];
+    out_row += (bag - t * a.bags_per_table) * a.out_stride + t * a.out_table_stride;
+  } else {
+    out_row += bag * a.out_stride;
+  }
+  const uint64_t row_bytes = a.row_bytes;
+  const uint64_t zero_row = (uint64_t)g_zero_row;
+  const int off = gl * VB;
+  const bool in_row = off < a.count * ES;
+
+  float acc[E];
+#pragma unroll
+  for (int c = 0; c < E; ++c) acc[c] = 0.0f;
+  float wsum = 0.0f;
+
+  for (int64_t k0 = s; k0 < e; k0 += G) {
+    const int64_t kk = k0 + gl;
+    uint32_t ridx = kNoRow;
+    float w = 0.0f;
+    if (kk < e) {
+      const int64_t key = load_key(a.keys, a.key_bytes, kk);
+      if ((uint64_t)key < num_rows) ridx = (uint32_t)key;  // keys outside the table read nothing
+      if (W) w = load_weight(a.weights, a.weight_dtype, kk);
+    }
+    const int n = (int)((e - k0) < G ? (e - k0) : G);
+    auto batch = [&](auto jc) {
+      constexpr int j0 = decltype(jc)::value;
+      if (j0 >= n) return;
+      uint32_t ri[U];
+      float wu[U];
+      group_bcast_batch<G, U, W, j0>(ridx, w, lane, ri, wu);
+      Vec<VB> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool real = ri[u] != kNoRow && in_row;
+        const uint64_t addr = real ? table + (uint64_t)ri[u] * row_bytes + (uint64_t)off
+                                   : zero_row + (uint64_t)(off & kZeroRowMask);
+        v[u] = load_vec<VB>(addr);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool use = j0 + u < n;
+        if (W && use) wsum += wu[u];
+        const bool add = use && in_row && ri[u] != kNoRow;
+        float x[E];
+        Meta m{1.0f, 0.0f};
+        decode<SDT, VB>(v[u], m, x);
+#pragma unroll
+        for (int c = 0; c < E; ++c) {
+          const float t = W ? __builtin_fmaf(x[c], wu[u], acc[c]) : acc[c] + x[c];
+          acc[c] = add ? t : acc[c];
+        }
+      }
+    };
+    for_batches<U, 0, G / U>(batch);
+  }
+
+  if (live && in_row) {
+    if (a.mean) {
+      const float d = W ? wsum : (float)(e - s);
+#pragma unroll
+      for (int c = 0; c < E; ++c) acc[c] = (d == 0.0f) ? 0.0f : acc[c] / d;
+    }
+    const bool out_f16 = a.out_dtype == kF16;
+    store_out<E>(out_row + (int64_t)gl * E * (out_f16 ? 2 : 4), acc, out_f16);
+  }
+}
+
+template <int SDT, int G, bool MT>
+hipError_t launch_short_g(const PoolLaunch& a, hipStream_t stream) {
+  typename std::conditional<MT, ShortArgsMT, ShortArgs>::type s{};
+  s.keys = a.keys;
+  s.offsets = a.offsets;
+  s.weights = a.weights;
+  s.out = a.out;
+  s.table = a.src.table;
+  s.num_keys = a.num_keys;
+  s.num_bags = a.num_bags;
+  s.hotness = a.hotness;
+  s.row_bytes = a.src.row_bytes;
+  s.num_rows = a.src.num_rows;
+  s.count = a.count;
+  s.out_stride = a.out_stride;
+  s.bags_per_table = a.bags_per_table;
+  s.out_table_stride = a.out_table_stride;
+  s.key_bytes = a.key_bytes;
+  s.weight_dtype = a.weight_dtype;
+  s.mean = a.mean;
+  s.out_dtype = a.out_dtype;
+  if constexpr (MT) {
+    for (int t = 0; t < a.num_tables; ++t) {
+      s.tables[t] = a.tables[t];
+      s.table_rows[t] = (uint32_t)a.table_rows[t];
+    }
+  }
+  const int64_t per_wg = 256 / G;
+  const dim3 grid((unsigned)((a.num_bags + per_wg - 1) / per_wg)), block(256);
+  // bags of a few dozen keys: 4 loads in flight per lane keep more waves
+  // resident, which hides the latency chain of each bag (offsets -> keys ->
+  // rows) better than wider batches (measured on 26-table, Poisson(20) bags:
+  // 4 -> 124 us, 8 -> 130 us, 16 -> 147 us, 2 -> 128 us); longer bags keep 16
+  const int64_t avg = a.keys_per_bag > 0 ? a.keys_per_bag
+                                         : a.num_keys / (a.num_bags > 0 ? a.num_bags : 1);
+  const bool narrow = avg <= 48;
+  if (a.weighted) {
+    if (narrow)
+      hipLaunchKernelGGL((pool_short_kernel<SDT, G, true, MT, 4>), grid, block, 0, stream, s);
+    else
+      hipLaunchKernelGGL((pool_short_kernel<SDT, G, true, MT, 16>), grid, block, 0, stream, s);
+  } else {
+    if (narrow)
+      hipLaunchKernelGGL((pool_short_kernel<SDT, G, false, MT, 4>), grid, block, 0, stream, s);
+    else
+      hipLaunchKernelGGL((pool_short_kernel<SDT, G, false, MT, 16>), grid, block, 0, stream, s);
+  }
+  return hipGetLastError();
+}
+
+template <int SDT, bool MT>
+hipError_t launch_short_sdt(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
+  switch (g.g) {
+    case 8: return launch_short_g<SDT, 8, MT>(a, stream);
+    case 16: return launch_short_g<SDT, 16, MT>(a, stream);
+    case 32: return launch_short_g<SDT, 32, MT>(a, stream);
+    case 64: return launch_short_g<SDT, 64, MT>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
+
+bool pool_short_eligible(const PoolLaunch& a, const PoolGeometry& g) {
+  if (a.src.cache_data != nullptr || !a.src.load_indices) return false;
+  if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
+  if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;
+  if (g.vb != 16 || g.passes != 1 || g.gpb != 1 || g.g < 8 || g.g > 64) return false;
+  if (a.num_tables > 0) {
+    for (int t = 0; t < a.num_tables; ++t)
+      if (a.tables[t] == nullptr || a.table_rows[t] == 0 || a.table_rows[t] >= kNoRow) return false;
+  } else if (a.src.table == nullptr || a.src.num_rows == 0 || a.src.num_rows >= kNoRow) {
+    return false;
+  }
+  return a.num_bags <= 0x7fffffffLL * (256 / g.g);
+}
+
+hipError_t launch_pool_short(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
+  const bool mt = a.num_tables > 0;
+  if (a.stored_dtype == kF16)
+    return mt ? launch_short_sdt<kF16, true>(a, g, stream) : launch_short_sdt<kF16, false>(a, g, stream);
+  if (a.stored_dtype == kF32)
+    return mt ? launch_short_sdt<kF32, true>(a, g, stream) : launch_short_sdt<kF32, false>(a, g, stream);
+  return hipErrorInvalidValue;
+}
 
 bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g) {
   if (a.src.cache_data != nullptr || a.num_tables > 0 || !a.src.load_indices) return false;

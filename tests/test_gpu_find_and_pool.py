@@ -231,3 +231,28 @@ def test_long_bag_kernel_csr_empty_and_int32():
     ref = oracle_pool(tb, keys, O.F32, dim, O.CSR, O.MEAN, off, bags, 0, None, 0, O.F32)
     assert rel_close(res[0], ref, 1e-5)
     assert np.all(res[0][lens == 0] == 0)
+
+
+@pytest.mark.parametrize("dtype,dim", [(O.F16, 64), (O.F16, 128), (O.F32, 128), (O.F16, 512), (O.F32, 256)])
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WSUM, _lib.POOL_WMEAN])
+def test_short_bag_kernel_matches_general_kernel_and_oracle(dtype, dim, pooling):
+    """Short CSR bags over a linear f16/f32 table take the lean short-bag
+    kernel (unroll hint 0); an unroll hint forces the general kernel.  One
+    lane group per bag in key order, so both equal the key-order oracle bit
+    for bit; empty bags and keys outside the table included."""
+    rng = np.random.default_rng(2000 + dim + 11 * pooling)
+    rows, bags = 20000, 700
+    tb = float_table(rng, rows, dim, dtype, dyadic_values=False)
+    off = csr_offsets(rng, bags, 45)
+    keys = rng.integers(0, rows, size=int(off[-1])).astype(np.int64)
+    keys[rng.uniform(size=keys.size) < 0.02] = rows + 3
+    weighted = pooling in (_lib.POOL_WSUM, _lib.POOL_WMEAN)
+    w = rng.uniform(0, 1, size=keys.size).astype(np.float32) if weighted else None
+    got = [run_pool(tb, dtype, keys, pooling, _lib.SPARSE_CSR, off, bags, 0, w, O.F32, dtype, 0, unroll)
+           for unroll in (0, 8)]
+    bits = np.uint16 if dtype == O.F16 else np.uint32
+    assert np.array_equal(got[0].view(bits), got[1].view(bits))
+    padded = np.concatenate([tb, np.zeros((1, tb.shape[1]), np.uint8)])
+    mapped = np.where(keys < rows, keys, rows)
+    ref = oracle_pool(padded, mapped, dtype, dim, O.CSR, pooling, off, bags, 0, w, O.F32, dtype)
+    assert np.array_equal(got[0].view(bits), ref.view(bits))

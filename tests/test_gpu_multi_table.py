@@ -33,17 +33,18 @@ def make_inputs(rng, num_tables, batch, dim, dtype, card_lo=1000, card_hi=100000
     return tabs, off, keys, w
 
 
-def run_multi(tabs, off, keys, w, batch, dtype, pooling, out_dtype):
+def run_multi(tabs, off, keys, w, batch, dtype, pooling, out_dtype, bounded=True, wdt=_lib.DT_F32):
     T = len(tabs)
     width = tabs[0].shape[1]
     count = (width - O.meta_bytes(dtype)) // O.value_bytes(dtype)
     d_tabs = [to_dev(t.reshape(-1)) for t in tabs]
     ptrs = (ctypes.c_void_p * T)(*[d.data_ptr() for d in d_tabs])
+    rows = (ctypes.c_int64 * T)(*[t.shape[0] for t in tabs]) if bounded else None
     d_keys, d_off, d_w = to_dev(keys), to_dev(off), to_dev(w)
     oes = 2 if out_dtype == O.F16 else 4
     out = torch.zeros((batch, T * count * oes), dtype=torch.uint8, device="cuda")
-    _lib.call("nve_amd_find_and_pool_multi", _lib.KEY_INT64, T, ptrs, width, CDT[dtype], batch, keys.size,
-              vp(d_keys), vp(d_off), vp(d_w), _lib.DT_F32, pooling, CDT[out_dtype], vp(out), stream_ptr())
+    _lib.call("nve_amd_find_and_pool_multi", _lib.KEY_INT64, T, ptrs, rows, width, CDT[dtype], batch,
+              keys.size, vp(d_keys), vp(d_off), vp(d_w), wdt, pooling, CDT[out_dtype], vp(out), stream_ptr())
     torch.cuda.synchronize()
     return out.cpu().numpy().view(np.uint16 if out_dtype == O.F16 else np.float32).reshape(batch, T, count)
 
@@ -82,3 +83,47 @@ def test_more_tables_than_one_launch_and_quantized_rows():
     got = run_multi(tabs, off, keys, w, batch, O.XI8A_F32, _lib.POOL_WMEAN, O.F32)
     ref = oracle_multi(tabs, off, keys, w, batch, O.XI8A_F32, _lib.POOL_WMEAN, O.F32)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("bounded", [True, False])
+def test_unbounded_tables_take_the_general_kernel_with_the_same_bits(bounded):
+    """Without row counts the launch keeps the general kernel (no bound check,
+    64-bit row indices); with them the short-bag kernel runs.  Same sums."""
+    rng = np.random.default_rng(91)
+    batch, dim = 256, 128
+    tabs, off, keys, w = make_inputs(rng, 5, batch, dim, O.F16)
+    got = run_multi(tabs, off, keys, w, batch, O.F16, _lib.POOL_WMEAN, O.F32, bounded=bounded)
+    ref = oracle_multi(tabs, off, keys, w, batch, O.F16, _lib.POOL_WMEAN, O.F32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_keys_outside_their_table_read_nothing():
+    """With row counts, a key outside its own table adds nothing (the bag's
+    Mean still counts it), checked against the oracle on tables padded with a
+    zero row; fp32 tables, f16 weights."""
+    rng = np.random.default_rng(93)
+    batch, dim = 128, 64
+    tabs, off, keys, w = make_inputs(rng, 4, batch, dim, O.F32)
+    bad = rng.random(keys.size) < 0.05
+    keys = keys.copy()
+    keys[bad] = 10**9
+    mapped = keys.copy()
+    padded = []
+    for t in range(len(tabs)):
+        lo, hi = off[t * batch], off[(t + 1) * batch]
+        rows = tabs[t].shape[0]
+        mapped[lo:hi] = np.where(keys[lo:hi] < rows, keys[lo:hi], rows)
+        padded.append(np.concatenate([tabs[t], np.zeros((1, tabs[t].shape[1]), np.uint8)]))
+    w16 = w.astype(np.float16)
+    for pooling in (_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WSUM):
+        got = run_multi(tabs, off, keys, w16, batch, O.F32, pooling, O.F32, wdt=_lib.DT_F16)
+        res = []
+        for t in range(len(tabs)):
+            lo, hi = off[t * batch], off[(t + 1) * batch]
+            loc = off[t * batch:(t + 1) * batch + 1] - lo
+            ptrs = O.linear_row_ptrs(mapped[lo:hi], np.ascontiguousarray(padded[t]).reshape(-1),
+                                     padded[t].shape[1])
+            res.append(O.pool(ptrs, O.F32, dim, O.CSR, pooling, hi - lo, loc, batch, 0,
+                              w16[lo:hi].view(np.uint16), O.F16, O.F32))
+        ref = np.stack(res, axis=1)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
