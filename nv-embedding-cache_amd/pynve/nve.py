@@ -15,8 +15,10 @@ accessed-by the GPUs, memblock.cpp:111-134) is pinned host memory here: with
 XNACK off, that is the memory the MI355X reads over the host link without
 page faults, which is what the reference's advice arranges.
 
-Out of this build (raise NotImplementedInBuild): `update` / `accumulate` on GPU tables,
-HostEmbedding / HierarchicalEmbedding layers, the parameter-server tables and
+Table checkpoints (`TensorFileFormat`, `write_tensor_to_stream`,
+`load_tensor_from_stream`) read and write the reference's .nve container.
+
+Out of this build (raise NotImplementedInBuild): HostEmbedding / HierarchicalEmbedding layers, the parameter-server tables and
 the multi-process memory blocks (NVL / MPI / Dist*).
 """
 import ctypes
@@ -206,6 +208,22 @@ class LinearMemBlock(MemBlock):
             import torch
             self._tensor = torch.empty(size, dtype=torch.uint8, device=f"cuda:{self.device_id}")
             super().__init__(MemBlockType.Linear, self._tensor.data_ptr(), size)
+
+
+def resolve_memblock_devices(type, def_index, override=()):
+    """GPU ids to rebuild a memory block with (memblock.cpp:144-165): `override`
+    when given, else every GPU from def_index on for an NVL block, else
+    [def_index]."""
+    if len(override):
+        return list(override)
+    if MemBlockType(type) == MemBlockType.NVL:
+        import torch
+        n = torch.cuda.device_count()
+        if not 0 <= int(def_index) < n:
+            raise _lib.NVEError(_lib.RUNTIME, f"resolve_memblock_devices: def_index={def_index} "
+                                f"out of range, system has {n} GPUs")
+        return list(range(int(def_index), n))
+    return [int(def_index)]
 
 
 def _not_in_build(what):
@@ -399,6 +417,7 @@ class GPUEmbedding(NVEmbedBinding):
         config = config if config is not None else EmbedLayerConfig()
         super().__init__(device_id, row_size, dtype, config)
         self.num_embeddings_ = int(num_embeddings)
+        self.row_size_ = int(row_size)
         self.mem_block_ = mem_block
         cfg = _lib.load().nve_gpu_embedding_layer_config_default()
         cfg.layer_name = b"gpu_layer"
@@ -502,6 +521,245 @@ class HostEmbedding(NVEmbedBinding):
 class HierarchicalEmbedding(NVEmbedBinding):
     def __init__(self, *args, **kwargs):
         _not_in_build("HierarchicalEmbedding (host / remote tiers)")
+
+
+# ---------------------------------------------------------------------------
+# table checkpoints: the .nve container (serialization.hpp:100-140,
+# serialization.cpp:234-300) over a Python binary stream
+# ---------------------------------------------------------------------------
+
+class _PyStream:
+    """A binary Python stream as the format reads and writes it
+    (binding_serialization.cpp:22-70): `write` repeats until the stream has
+    taken every byte, `read` repeats `readinto` until it returns 0."""
+
+    def __init__(self, stream):
+        self._s = stream
+
+    def write(self, data):
+        mv = memoryview(data).cast("B")
+        done = 0
+        while done < len(mv):
+            n = self._s.write(mv[done:])
+            done += len(mv) - done if n is None else int(n)
+
+    def read_into(self, mv):
+        mv = memoryview(mv).cast("B")
+        total = 0
+        while total < len(mv):
+            n = self._s.readinto(mv[total:])
+            if not n:
+                break
+            total += int(n)
+        return total
+
+    def seek(self, pos):
+        return self._s.seek(int(pos))
+
+    def tell(self):
+        return int(self._s.tell())
+
+    def size(self):
+        cur = self._s.tell()
+        end = self._s.seek(0, 2)
+        self._s.seek(cur)
+        return int(end)
+
+    def flush(self):
+        self._s.flush()
+
+
+class TensorFileFormat:
+    """The NVE table file (serialization.hpp:110-140): a 12-byte header
+    {u32 magic 0x4E564500, u32 version major 0, u32 minor 2} at offset 0, then
+    entries, each a 32-byte record {u64 key1, u64 name, u64 offset of the next
+    record, u64 length} followed by `length` bytes of row-major table data.
+    key1 packs the row width in elements (bits 0-15), the element size in bytes
+    (bits 16-19) and the row count (bits 20-63).  All fields little-endian,
+    the byte order the reference writes on x86 and aarch64 hosts."""
+
+    MAGIC_NUMBER = 0x4E564500
+    VERSION_MAJOR = 0
+    VERSION_MINOR = 2
+    ROW_SIZE_BITS = 16
+    DATA_TYPE_BITS = 4
+    ROWS_BITS = 64 - (ROW_SIZE_BITS + DATA_TYPE_BITS)
+    HEADER_BYTES = 12
+    ENTRY_BYTES = 32
+
+    @staticmethod
+    def _io(stream):
+        return stream if isinstance(stream, _PyStream) else _PyStream(stream)
+
+    def write_table_file_header(self, stream):
+        """serialization.cpp:234-241: header at offset 0, then flush."""
+        import struct
+        s = self._io(stream)
+        s.seek(0)
+        s.write(struct.pack("<III", self.MAGIC_NUMBER, self.VERSION_MAJOR, self.VERSION_MINOR))
+        s.flush()
+
+    def verify_table_header(self, stream):
+        """serialization.cpp:243-252: True when offset 0 holds this header;
+        leaves the stream at the first entry."""
+        import struct
+        s = self._io(stream)
+        s.seek(0)
+        buf = bytearray(self.HEADER_BYTES)
+        if s.read_into(buf) != self.HEADER_BYTES:
+            return False
+        return struct.unpack("<III", buf) == (self.MAGIC_NUMBER, self.VERSION_MAJOR,
+                                               self.VERSION_MINOR)
+
+    def make_key(self, rows, cols, element_size):
+        """key1 of an entry, with the reference's limits (serialization.cpp:284-293)."""
+        rows, cols, element_size = int(rows), int(cols), int(element_size)
+        if not 0 <= cols < (1 << self.ROW_SIZE_BITS):
+            raise _lib.NVEError(_lib.RUNTIME, "nve support max 16 bit row size")
+        if not 0 <= rows < (1 << self.ROWS_BITS):
+            raise _lib.NVEError(_lib.RUNTIME, "nve support max 44 bit rows")
+        if not 0 <= element_size < (1 << self.DATA_TYPE_BITS):
+            raise _lib.NVEError(_lib.RUNTIME, "nve support max 2 bit data type")
+        return cols | (element_size << self.ROW_SIZE_BITS) | (rows << (self.ROW_SIZE_BITS +
+                                                                      self.DATA_TYPE_BITS))
+
+    def write_tensor_to_stream(self, stream, name, rows, cols, element_size, chunks):
+        """Append one entry at the stream's position (serialization.cpp:254-264);
+        `chunks` yields the rows*cols*element_size data bytes in order."""
+        import struct
+        s = self._io(stream)
+        name = _u64_name(name)
+        key1 = self.make_key(rows, cols, element_size)
+        sz = int(rows) * int(cols) * int(element_size)
+        s.write(struct.pack("<QQQQ", key1, name, sz + self.ENTRY_BYTES + s.tell(), sz))
+        written = 0
+        for c in chunks:
+            s.write(c)
+            written += memoryview(c).nbytes
+        if written != sz:
+            raise _lib.NVEError(_lib.RUNTIME, f"tensor source gave {written} of {sz} bytes")
+        s.flush()
+
+    def find_tensor(self, stream, name, rows, cols, element_size):
+        """The search of load_tensor_from_stream (serialization.cpp:266-282):
+        verify the header, then walk the entries from the first; on the entry
+        named `name` check its length and return it with the stream at its data.
+        Returns None when the stream ends first (no error, as in the reference)."""
+        import struct
+        s = self._io(stream)
+        name = _u64_name(name)
+        if not self.verify_table_header(s):
+            raise _lib.NVEError(_lib.RUNTIME, "Incorrect file version")
+        sz = int(rows) * int(cols) * int(element_size)
+        rec = bytearray(self.ENTRY_BYTES)
+        got = s.read_into(rec)
+        while got != 0:
+            if got != self.ENTRY_BYTES:
+                raise _lib.NVEError(_lib.RUNTIME, "Problem reading table entry")
+            key1, key2, offset, length = struct.unpack("<QQQQ", rec)
+            if key2 == name:
+                if length != sz:
+                    raise _lib.NVEError(_lib.RUNTIME, "Incorrect tensor size")
+                # a truncated entry fails here, before the destination is touched
+                if s.tell() + length > s.size():
+                    raise _lib.NVEError(_lib.RUNTIME, "Problem reading tensor")
+                return (key1, key2, offset, length)
+            s.seek(offset)
+            got = s.read_into(rec)
+        return None
+
+
+def _u64_name(name):
+    name = int(name)
+    if not 0 <= name < (1 << 64):
+        raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, f"tensor name {name} is not a uint64")
+    return name
+
+
+_STAGE_BYTES = 64 << 20
+
+
+def _host_view(ptr, nbytes):
+    return memoryview((ctypes.c_char * nbytes).from_address(ptr)).cast("B") if nbytes else memoryview(b"")
+
+
+def _table_geometry(layer):
+    """(rows, row width in elements, element size, base address) of the table a
+    layer checkpoints: the backing table of a LinearUVMEmbedding (element size
+    4 for Float32 tables, else 2: binding_layers.hpp:586-590) or the device
+    table of a GPUEmbedding (dtype_size: binding_layers.hpp:677-680)."""
+    if isinstance(layer, LinearUVMEmbedding):
+        esize = 4 if layer.data_type_ == DataType_t.Float32 else 2
+        return layer.num_embeddings_, layer.row_size_, esize, layer.mem_block_.get_ptr()
+    if isinstance(layer, GPUEmbedding):
+        return (layer.num_embeddings_, layer.row_size_, dtype_size(layer.data_type_),
+                layer.mem_block_.get_ptr())
+    raise TypeError("write_tensor_to_stream / load_tensor_from_stream take a LinearUVMEmbedding "
+                    f"or a GPUEmbedding, not {type(layer).__name__}")
+
+
+def _device_chunks(layer, base, nbytes):
+    """The GPU table's bytes in order, through a pinned staging buffer (bounded
+    host memory, unlike the reference's one full-size copy)."""
+    import torch
+    torch.cuda.synchronize(layer.device_id_)  # pending lookups / updates land first
+    stage = _PinnedHost(MemBlockType.Host, min(nbytes, _STAGE_BYTES))
+    view = _host_view(stage.get_ptr(), stage.get_size_in_bytes())
+    done = 0
+    while done < nbytes:
+        n = min(nbytes - done, _STAGE_BYTES)
+        rc = _hip_lib().hipMemcpy(stage.get_ptr(), base + done, n, 4)
+        if rc != 0:
+            raise _lib.NVEError(_lib.HIP_ERROR, f"table read: hipMemcpy failed ({rc})")
+        yield view[:n]
+        done += n
+
+
+def write_tensor_to_stream(layer, stream, name):
+    """Append the layer's table to `stream` as one entry named `name`
+    (python_binding.cu:83-99; binding_layers.hpp:626-630 and 693-703).  The
+    stream must already hold the header (TensorFileFormat.write_table_file_header)."""
+    rows, cols, esize, base = _table_geometry(layer)
+    nbytes = rows * cols * esize
+    fmt = TensorFileFormat()
+    if isinstance(layer, LinearUVMEmbedding):
+        fmt.write_tensor_to_stream(stream, name, rows, cols, esize, [_host_view(base, nbytes)])
+    else:
+        fmt.write_tensor_to_stream(stream, name, rows, cols, esize, _device_chunks(layer, base, nbytes))
+
+
+def load_tensor_from_stream(layer, stream, name):
+    """Fill the layer's table from the entry named `name` of `stream`
+    (python_binding.cu:89-105; binding_layers.hpp:632-636 and 705-716).
+
+    Errors as in the reference: a wrong header, a short entry record or an entry
+    of another size raise.  A stream without the name leaves a LinearUVMEmbedding's
+    table as it was and zero-fills a GPUEmbedding's table (the reference copies
+    its zero-initialised host buffer to the device either way).  Rows already in
+    a LinearUVMEmbedding's GPU cache are not refreshed, as in the reference."""
+    rows, cols, esize, base = _table_geometry(layer)
+    nbytes = rows * cols * esize
+    s = _PyStream(stream)
+    found = TensorFileFormat().find_tensor(s, name, rows, cols, esize)
+    if isinstance(layer, LinearUVMEmbedding):
+        if found is not None and s.read_into(_host_view(base, nbytes)) != nbytes:
+            raise _lib.NVEError(_lib.RUNTIME, "Problem reading tensor")
+        return
+    import torch
+    torch.cuda.synchronize(layer.device_id_)
+    stage = _PinnedHost(MemBlockType.Host, min(nbytes, _STAGE_BYTES))
+    view = _host_view(stage.get_ptr(), stage.get_size_in_bytes())
+    if found is None:
+        ctypes.memset(stage.get_ptr(), 0, stage.get_size_in_bytes()) if nbytes else None
+    done = 0
+    while done < nbytes:
+        n = min(nbytes - done, _STAGE_BYTES)
+        if found is not None and s.read_into(view[:n]) != n:
+            raise _lib.NVEError(_lib.RUNTIME, "Problem reading tensor")
+        rc = _hip_lib().hipMemcpy(base + done, stage.get_ptr(), n, 4)
+        if rc != 0:
+            raise _lib.NVEError(_lib.HIP_ERROR, f"table write: hipMemcpy failed ({rc})")
+        done += n
 
 
 def get_dl_tensor(layer, dtype=None):

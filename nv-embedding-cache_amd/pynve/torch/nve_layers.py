@@ -14,7 +14,6 @@ from typing import Optional
 
 import torch
 
-from .. import _lib
 from .. import nve
 from . import HAS_TORCH_OPS
 from . import nve_ops
@@ -245,8 +244,9 @@ class NVEmbeddingBase(torch.nn.Module):
                              _current_stream_handle(self.device))
 
     def load_from_stream(self, stream):
-        raise _lib.NotImplementedInBuild(_lib.NOT_IMPLEMENTED,
-                                         "Table checkpoint I/O is not part of this build")
+        """Fill the table from the .nve entry named by this module's id
+        (nve_layers.py:400-401)."""
+        nve.load_tensor_from_stream(self.emb_layer, stream, self.id)
 
 
 class NVEmbedding(NVEmbeddingBase):
