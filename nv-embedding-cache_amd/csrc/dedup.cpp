@@ -61,7 +61,8 @@ size_t dedup_workspace_bytes(int64_t n) {
 }
 
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
-                  void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s) {
+                  void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
+                  uint32_t* pos_key) {
   if (n <= 0) return 0;
   NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
   NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
@@ -77,7 +78,8 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   const uint32_t* vs = alt ? b.vb : b.va;
   NVE_HIP(launch_run_heads(ks, n, b.heads, s));
   NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, b.sort_tmp, s));
-  NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, s));
+  NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start,
+                               pos_key, s));
   const uint32_t u = read_back(b.total, s);
   NVE_HIP(launch_dedup_counts(b.start, u, key_bytes, counts, s));
   return (int64_t)u;

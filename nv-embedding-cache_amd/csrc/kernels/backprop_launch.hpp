@@ -12,14 +12,39 @@ enum { kBackpropConcat = 0, kBackpropSum = 1, kBackpropWSum = 2, kBackpropMean =
 hipError_t launch_bag_denom(const void* offsets, int key_bytes, int64_t num_bags, int64_t hotness,
                             const void* weights, int wdt, int wmean, float* denom,
                             hipStream_t stream);
+// Dedup positions outside every bag read no gradient row.
+constexpr uint32_t kNoGradRow = 0xffffffffu;
+// Positions per block of the summation order (a piece is one key's positions
+// inside one block), and the number of sub-sequences a key's pieces are added
+// in before their sums are added.
+constexpr int kPieceBlock = 32;
+constexpr int kPieceFanIn = 8;
+constexpr int kCombineBlocks = 8;  // block entries per combine workgroup
+constexpr int kLightPieces = 32;   // a crossing key of more pieces is added by a whole workgroup
+
 hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, int mode,
                                 const void* offsets, int64_t num_bags, int64_t hotness,
-                                const void* weights, int wdt, const float* denom, int64_t none_row,
-                                void* rowkey, float* nw, hipStream_t stream);
-hipError_t launch_run_count(const void* counts, int key_bytes, int64_t u, int64_t max_run,
-                            uint32_t* nruns, hipStream_t stream);
-hipError_t launch_run_write(const void* doff, int key_bytes, int64_t u, int64_t n, int64_t max_run,
-                            const uint32_t* run_scan, uint32_t total, void* run_off, void* key_run_off,
-                            hipStream_t stream);
+                                const void* weights, int wdt, const float* denom, uint32_t* rows,
+                                float* nw, hipStream_t stream);
+
+struct PieceArgs {
+  const uint32_t* kidx;  // unique index of each dedup position
+  const uint32_t* rows;  // gradient row of each dedup position (kNoGradRow: none)
+  const float* nw;       // weight of each dedup position (weighted modes)
+  const void* doff;      // first dedup position of each unique key (key type)
+  const void* counts;    // positions of each unique key (key type)
+  const uint8_t* grads;  // gradient rows, dim elements of the gradient type
+  float* slots;          // two fp32 rows per block
+  uint32_t* cross;       // per block: the key that starts in it and crosses out, or none
+  uint8_t* out;          // one row per unique key, of the gradient type
+  int64_t n;
+  int32_t dim;
+  int32_t key_bytes;
+};
+
+// Pieces: rows of keys inside one block, fp32 partial rows of the others.
+hipError_t launch_piece_pool(const PieceArgs& a, int f16, int weighted, hipStream_t stream);
+// The keys that cross a block edge, from their pieces.
+hipError_t launch_piece_combine(const PieceArgs& a, int f16, hipStream_t stream);
 
 }  // namespace nve_amd

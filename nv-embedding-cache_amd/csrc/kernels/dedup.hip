@@ -27,11 +27,12 @@ __global__ __launch_bounds__(256) void dedup_outputs_kernel(const uint64_t* ks, 
                                                             const uint32_t* scan, int64_t n,
                                                             int key_bytes, void* unique,
                                                             void* inverse, void* offsets,
-                                                            uint32_t* start) {
+                                                            uint32_t* start, uint32_t* pos_key) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   store_key(inverse, key_bytes, i, (int64_t)vs[i]);
   const bool head = (i == 0 || ks[i] != ks[i - 1]);
+  if (pos_key != nullptr) pos_key[i] = head ? scan[i] : scan[i] - 1u;  // unique index of position i
   if (head) {
     const uint32_t u = scan[i];
     store_key(unique, key_bytes, u, unflip_key(ks[i], key_bytes));
@@ -57,10 +58,11 @@ hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int fli
 
 hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan,
                                 int64_t n, int key_bytes, void* unique, void* inverse,
-                                void* offsets, uint32_t* start, hipStream_t stream) {
+                                void* offsets, uint32_t* start, uint32_t* pos_key,
+                                hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(dedup_outputs_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, vs, scan,
-                     n, key_bytes, unique, inverse, offsets, start);
+                     n, key_bytes, unique, inverse, offsets, start, pos_key);
   return hipGetLastError();
 }
 

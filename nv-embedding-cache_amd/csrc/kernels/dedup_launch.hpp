@@ -11,7 +11,8 @@ hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int fli
                              uint32_t* v, hipStream_t stream);
 hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan,
                                 int64_t n, int key_bytes, void* unique, void* inverse,
-                                void* offsets, uint32_t* start, hipStream_t stream);
+                                void* offsets, uint32_t* start, uint32_t* pos_key,
+                                hipStream_t stream);
 hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, int key_bytes, void* counts,
                                hipStream_t stream);
 

@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "device_common.cuh"
+#include "lane_moves.cuh"
 #include "pool_launch.hpp"
 
 namespace nve_amd {
@@ -34,33 +35,6 @@ namespace nve_amd {
 namespace {
 
 constexpr uint32_t kNoRow = 0xffffffffu;
-
-// DPP controls (row = 16 lanes)
-constexpr int kDppRowNewBcast = 0x150;  // + n: every lane of a row reads lane n of that row
-constexpr int kDppRowRor8 = 0x128;      // lane l reads lane (l + 8) mod 16 of its row: l ^ 8
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
-}
-
-// Value of lane J of this lane's G-lane group (groups aligned to G lanes).
-template <int G, int J>
-__device__ __forceinline__ uint32_t group_bcast(uint32_t v, int lane) {
-  if constexpr (G == 64) {
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, J);
-  } else if constexpr (G == 16) {
-    return dpp_mov<kDppRowNewBcast + J>(v);
-  } else if constexpr (G == 8) {
-    const uint32_t lo = dpp_mov<kDppRowNewBcast + J>(v);
-    const uint32_t hi = dpp_mov<kDppRowNewBcast + 8 + J>(v);
-    return (lane & 8) ? hi : lo;
-  } else {  // G == 32: lane J % 16 of each row, then the even or odd row of each pair
-    const uint32_t b = dpp_mov<kDppRowNewBcast + (J & 15)>(v);
-    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-    return J < 16 ? r[0] : r[1];
-  }
-}
 
 // a + (a of lane l ^ M), the same float addition as a + __shfl_xor(a, M)
 // (addition commutes exactly, so both partners get the same bits).
@@ -87,15 +61,6 @@ __device__ __forceinline__ void group_bcast_batch(uint32_t ridx, float w, int la
     ri[u] = group_bcast<G, J0 + u>(ridx, lane);
     wu[u] = W ? __uint_as_float(group_bcast<G, J0 + u>(__float_as_uint(w), lane)) : 1.0f;
     group_bcast_batch<G, U, W, J0, u + 1>(ridx, w, lane, ri, wu);
-  }
-}
-
-// f(integral_constant<int, b * U>) for b = B .. NB - 1, unrolled at compile time
-template <int U, int B, int NB, typename F>
-__device__ __forceinline__ void for_batches(F& f) {
-  if constexpr (B < NB) {
-    f(std::integral_constant<int, B * U>{});
-    for_batches<U, B + 1, NB>(f);
   }
 }
 

@@ -1131,12 +1131,15 @@ static int64_t bag_of_pos(int64_t p, int sparse, const void* offsets, int key_by
   return p < load_key(offsets, key_bytes, lo + 1) ? lo : -1;
 }
 
+#define PIECE_FAN_IN 8 /* sub-sequences of a key's pieces */
+
 int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int pooling, int sparse,
                              const void* offsets, int64_t num_bags, int64_t hotness,
                              const void* weights, int weight_dtype, const void* grads_in,
-                             int grad_dtype, int64_t dim, int64_t max_run, void* unique_out,
+                             int grad_dtype, int64_t dim, int64_t block, void* unique_out,
                              void* grads_out) {
   if (n <= 0) return 0;
+  if (block < 1) block = 1;
   int64_t* uq = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
   int64_t* ct = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
   int64_t* inv = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
@@ -1167,30 +1170,42 @@ int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int poo
     }
   }
   float* part = (float*)malloc(sizeof(float) * (size_t)dim);
+  float* quarter = (float*)malloc(sizeof(float) * (size_t)dim);
   float* tot = (float*)malloc(sizeof(float) * (size_t)dim);
   for (int64_t k = 0; k < u; k++) {
+    /* pieces: key k's positions [d, e) of the dedup order cut at multiples of block */
+    const int64_t d = off[k], e = off[k] + ct[k];
+    const int64_t first_block = d / block;
+    const int64_t pieces = (e - 1) / block - first_block + 1;
+    const int64_t per_part = (pieces + PIECE_FAN_IN - 1) / PIECE_FAN_IN;
     for (int64_t c = 0; c < dim; c++) tot[c] = 0.0f;
-    for (int64_t r0 = 0; r0 < ct[k]; r0 += max_run) {
-      const int64_t r1 = (r0 + max_run < ct[k]) ? r0 + max_run : ct[k];
-      for (int64_t c = 0; c < dim; c++) part[c] = 0.0f;
-      for (int64_t j = r0; j < r1; j++) {
-        const int64_t p = inv[off[k] + j];
-        int64_t row;
-        float w = 1.0f;
-        if (concat) {
-          row = p;
-        } else {
-          row = bag_of_pos(p, sparse, offsets, key_bytes, num_bags, hotness);
-          if (row < 0) continue; /* a position in no bag adds nothing */
-          if (weighted) w = load_f(weights, weight_dtype, p);
-          if (normalized) w = (pooling == ORC_MEAN ? 1.0f : w) / denom[row];
+    for (int64_t q = 0; q < PIECE_FAN_IN; q++) {
+      for (int64_t c = 0; c < dim; c++) quarter[c] = 0.0f;
+      const int64_t j_end = (q + 1) * per_part < pieces ? (q + 1) * per_part : pieces;
+      for (int64_t j = q * per_part; j < j_end; j++) {
+        const int64_t b_lo = (first_block + j) * block, b_hi = b_lo + block;
+        const int64_t ps = d > b_lo ? d : b_lo, pe = e < b_hi ? e : b_hi;
+        for (int64_t c = 0; c < dim; c++) part[c] = 0.0f;
+        for (int64_t pos = ps; pos < pe; pos++) {
+          const int64_t p = inv[pos];
+          int64_t row;
+          float w = 1.0f;
+          if (concat) {
+            row = p;
+          } else {
+            row = bag_of_pos(p, sparse, offsets, key_bytes, num_bags, hotness);
+            if (row < 0) continue; /* a position in no bag adds nothing */
+            if (weighted) w = load_f(weights, weight_dtype, p);
+            if (normalized) w = (pooling == ORC_MEAN ? 1.0f : w) / denom[row];
+          }
+          for (int64_t c = 0; c < dim; c++) {
+            const float g = load_f(grads_in, grad_dtype, row * dim + c);
+            part[c] = (concat || pooling == ORC_SUM) ? part[c] + g : fmaf(g, w, part[c]);
+          }
         }
-        for (int64_t c = 0; c < dim; c++) {
-          const float g = load_f(grads_in, grad_dtype, row * dim + c);
-          part[c] = (concat || pooling == ORC_SUM) ? part[c] + g : fmaf(g, w, part[c]);
-        }
+        for (int64_t c = 0; c < dim; c++) quarter[c] = quarter[c] + part[c];
       }
-      for (int64_t c = 0; c < dim; c++) tot[c] = tot[c] + part[c];
+      for (int64_t c = 0; c < dim; c++) tot[c] = tot[c] + quarter[c];
     }
     for (int64_t c = 0; c < dim; c++) {
       if (grad_dtype == ORC_F16)
@@ -1204,6 +1219,7 @@ int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int poo
       ((int64_t*)unique_out)[k] = uq[k];
   }
   free(tot);
+  free(quarter);
   free(part);
   free(denom);
   free(off);

@@ -223,15 +223,19 @@ int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, co
  *   Concatenate: grads_in has one row per key position; grad(u) = sum of the
  *     rows of u's positions.
  * Order (defined here; the reference cuts runs at 1024 positions and adds the
- * pieces with atomics, so its order is not fixed): u's positions, ascending,
- * are cut into runs of max_run; a run is accumulated in fp32 in position order
- * (fmaf(g, nw, acc), or acc + g when unweighted: Sum, Concatenate), the runs'
- * fp32 partial rows are added in run order starting from 0, and the sum is
- * rounded once to grad_dtype.  Returns the number of unique keys. */
+ * pieces with atomics, so its order is not fixed): the positions of all keys,
+ * stably sorted by key (the dedup order), are cut at every multiple of `block`;
+ * a piece is one key's positions inside one block.  A piece is accumulated in
+ * fp32 in position order from 0 (fmaf(g, nw, acc), or acc + g when unweighted:
+ * Sum, Concatenate).  A key's J pieces are split into 8 consecutive
+ * sub-sequences of ceil(J / 8) pieces (the last ones may be short or empty);
+ * each adds its pieces' rows in order from 0, the key's row adds the 8 sums in
+ * order from 0, and the sum is rounded once to grad_dtype.  Returns the number
+ * of unique keys. */
 int64_t orc_pooling_backprop(const void* keys, int key_bytes, int64_t n, int pooling, int sparse,
                              const void* offsets, int64_t num_bags, int64_t hotness,
                              const void* weights, int weight_dtype, const void* grads_in,
-                             int grad_dtype, int64_t dim, int64_t max_run, void* unique_out,
+                             int grad_dtype, int64_t dim, int64_t block, void* unique_out,
                              void* grads_out);
 
 /* ---- dedup (deduper.cuh:136-221) ----

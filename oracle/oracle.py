@@ -382,9 +382,10 @@ def power_law(x, min_v, max_v, alpha):
 
 
 def pooling_backprop(keys, pooling, sparse, offsets, num_bags, hotness, weights, weight_dtype,
-                     grads_in, grad_dtype, dim, max_run=64):
+                     grads_in, grad_dtype, dim, block=32):
     """Sparse gradient (unique keys ascending, rows of grad_dtype bits) of a
-    lookup, in the run order documented in nve_oracle.h."""
+    lookup, in the summation order documented in nve_oracle.h (pieces of
+    `block`-aligned position blocks, eight sub-sequences per key)."""
     keys = np.ascontiguousarray(keys)
     n = keys.size
     if offsets is not None:
@@ -396,5 +397,5 @@ def pooling_backprop(keys, pooling, sparse, offsets, num_bags, hotness, weights,
     out = np.zeros((max(n, 1), dim), np.uint16 if grad_dtype == F16 else np.float32)
     u = lib().orc_pooling_backprop(_p(keys), keys.itemsize, n, pooling, sparse, _p(offsets), num_bags,
                                    hotness, _p(weights), weight_dtype, _p(grads_in), grad_dtype, dim,
-                                   max_run, _p(uq), _p(out))
+                                   block, _p(uq), _p(out))
     return uq[:u], out[:u]

@@ -2,12 +2,15 @@
 GradientCalculator::compute_gradients, cuda_ops/gradient_calculator.cuh:238-301)
 against the oracle (orc_pooling_backprop, itself pinned to torch autograd).
 
-Both sum each unique key's positions in runs of 64 (fp32, position order) and
-then the runs, rounding once, so unique keys and gradient rows must match bit
-for bit.  Cases follow tests/kernels/pooling_backprop_tests.cu: Concatenate /
-Sum / Mean / WeightedSum / WeightedMean, Fixed and CSR bags, int32 and int64
-keys, plus fp16 gradients, Zipf keys whose hottest key spans many runs, empty
-bags and positions outside every bag."""
+Both add each unique key's positions in pieces (its positions inside one
+32-position block of the dedup order, fp32, position order), then the pieces in
+eight sub-sequences and their sums in order, rounding once, so unique keys and
+gradient rows must match bit for bit.  Cases follow
+tests/kernels/pooling_backprop_tests.cu: Concatenate / Sum / Mean / WeightedSum
+/ WeightedMean, Fixed and CSR bags, int32 and int64 keys, plus fp16 gradients,
+Zipf keys whose hottest key spans many blocks, empty bags and positions outside
+every bag, row widths of every lane layout (odd widths, rows wider than one
+pass of a lane group) and unaligned gradient buffers."""
 import ctypes
 
 import numpy as np
@@ -85,7 +88,7 @@ def test_backprop_matches_oracle_bitwise(pooling, sparse, key_dtype, gdt):
     keys, offsets, n, w, g = make_case(rng, pooling, sparse, key_dtype, wdt, gdt)
     hot = 40
     counts = np.bincount(keys.astype(np.int64))
-    assert counts.max() > 64  # several runs for the hottest key
+    assert counts.max() > 64  # several pieces for the hottest key
     uq, out = gpu_backprop(keys, pooling, sparse, offsets, hot, w, wdt, g, gdt, g.shape[1])
     bags = 0 if pooling == O.CONCAT else (offsets.size - 1 if offsets is not None else n // hot)
     ruq, rout = O.pooling_backprop(keys, pooling, sparse, offsets, bags, hot, w, wdt,
@@ -124,3 +127,78 @@ def test_uniform_keys_one_run_each_large_batch():
     ruq, rout = O.pooling_backprop(keys, O.MEAN, O.FIXED, None, bags, hot, None, O.F32, g.view(np.uint16),
                                    O.F16, dim)
     assert np.array_equal(uq, ruq) and np.array_equal(out, rout)
+
+
+@pytest.mark.parametrize("dim", [1, 3, 7, 8, 12, 100, 128, 200, 300, 520, 1030])
+@pytest.mark.parametrize("gdt", [O.F32, O.F16])
+def test_row_widths(dim, gdt):
+    """Vector lanes (16-byte rows pieces) and scalar lanes, 8 to 64 lanes per
+    block, and rows wider than one lane group's pass (column chunks)."""
+    rng = np.random.default_rng(500 + dim + gdt)
+    bags, hot, rows = 40, 30, 700
+    keys = (rng.zipf(1.2, size=bags * hot) % rows).astype(np.int64)
+    g = rng.normal(0, 1, size=(bags, dim)).astype(np.float16 if gdt == O.F16 else np.float32)
+    w = rng.uniform(0.1, 1.0, size=bags * hot).astype(np.float32)
+    for pooling in (O.SUM, O.WMEAN):
+        ww = w if pooling == O.WMEAN else None
+        uq, out = gpu_backprop(keys, pooling, O.FIXED, None, hot, ww, O.F32, g, gdt, dim)
+        ruq, rout = O.pooling_backprop(keys, pooling, O.FIXED, None, bags, hot, ww, O.F32,
+                                       g.view(np.uint16) if gdt == O.F16 else g, gdt, dim)
+        bits = np.uint16 if gdt == O.F16 else np.uint32
+        assert np.array_equal(uq, ruq) and np.array_equal(out, rout.view(bits))
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 63, 64, 65, 127, 128, 4097])
+def test_block_edges(n):
+    """Batches ending inside, at and just past a block; one key over all of
+    them, and keys that start exactly on a block edge."""
+    rng = np.random.default_rng(600 + n)
+    dim = 16
+    keys = np.sort(rng.integers(0, max(n // 20, 1), size=n)).astype(np.int64)
+    keys[: min(n, 32)] = 0  # key 0 fills the first block exactly when n >= 32
+    g = rng.normal(0, 1, size=(n, dim)).astype(np.float32)
+    for ks in (keys, np.zeros(n, np.int64), rng.permutation(keys)):
+        uq, out = gpu_backprop(ks, O.CONCAT, O.FIXED, None, 1, None, O.F32, g, O.F32, dim)
+        ruq, rout = O.pooling_backprop(ks, O.CONCAT, O.FIXED, None, 0, 1, None, O.F32, g, O.F32, dim)
+        assert np.array_equal(uq, ruq) and np.array_equal(out, rout.view(np.uint32))
+
+
+def test_hot_keys_hundreds_of_blocks():
+    """The c2bwd shape in miniature: 131,072 keys, the hottest over 7000
+    positions (more than 200 pieces, all eight sub-sequences long)."""
+    rng = np.random.default_rng(611)
+    bags, hot, dim = 512, 256, 128
+    x = rng.random(bags * hot)
+    keys = (np.floor(x ** 6 * 5_000_000)).astype(np.int64)
+    assert np.bincount(keys).max() > 7000
+    g = rng.normal(0, 0.1, size=(bags, dim)).astype(np.float16)
+    uq, out = gpu_backprop(keys, O.SUM, O.FIXED, None, hot, None, O.F32, g, O.F16, dim)
+    ruq, rout = O.pooling_backprop(keys, O.SUM, O.FIXED, None, bags, hot, None, O.F32, g.view(np.uint16),
+                                   O.F16, dim)
+    assert np.array_equal(uq, ruq) and np.array_equal(out, rout)
+
+
+def test_unaligned_gradient_buffers_take_scalar_lanes():
+    rng = np.random.default_rng(613)
+    bags, hot, dim = 30, 20, 64
+    keys = (rng.zipf(1.3, size=bags * hot) % 200).astype(np.int64)
+    g = rng.normal(0, 1, size=(bags, dim)).astype(np.float32)
+    n = keys.size
+    wsb = ctypes.c_uint64()
+    _lib.call("nve_amd_backprop_workspace_size", n, bags, dim, ctypes.byref(wsb))
+    ws = torch.empty(int(wsb.value), dtype=torch.uint8, device="cuda")
+    d_keys = to_dev(keys)
+    d_g = torch.empty(g.nbytes + 4, dtype=torch.uint8, device="cuda")
+    d_g[4:].copy_(torch.from_numpy(g.reshape(-1).view(np.uint8)))  # 4-byte aligned, not 16
+    uq = torch.zeros(n, dtype=torch.int64, device="cuda")
+    out = torch.zeros(n * dim * 4 + 4, dtype=torch.uint8, device="cuda")
+    nu = ctypes.c_int64(-1)
+    _lib.call("nve_amd_pooling_backprop", _lib.KEY_INT64, n, vp(d_keys), _lib.POOL_SUM, _lib.SPARSE_FIXED,
+              None, 0, hot, None, _lib.DT_UNKNOWN, ctypes.c_void_p(d_g.data_ptr() + 4), _lib.DT_F32, dim,
+              vp(uq), ctypes.c_void_p(out.data_ptr() + 4), ctypes.byref(nu), vp(ws), wsb.value,
+              stream_ptr())
+    torch.cuda.synchronize()
+    u = nu.value
+    got = out[4:4 + u * dim * 4].cpu().numpy().view(np.uint32).reshape(u, dim)
+    ruq, rout = O.pooling_backprop(keys, O.SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim)
+    assert np.array_equal(uq.cpu().numpy()[:u], ruq) and np.array_equal(got, rout.view(np.uint32))

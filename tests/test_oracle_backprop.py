@@ -95,20 +95,20 @@ def test_dyadic_sums_are_exact(pooling):
     keys = (rng.zipf(1.2, size=bags * hot) % rows).astype(np.int64)
     g = dyadic(rng, (bags * hot if pooling == CONCAT else bags, dim))
     uq, out = O.pooling_backprop(keys, pooling, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim,
-                                 max_run=5)
+                                 block=5)
     ref = dense_grad_torch(keys, pooling, O.FIXED, None, bags, hot, None, g, rows)
     assert np.array_equal(sparse_to_dense(uq, out, rows, O.F32), ref)
 
 
 def test_run_length_only_regroups():
-    """max_run changes the grouping of the additions, not the sum: exact for
+    """The block size changes the grouping of the additions, not the sum: exact for
     dyadic values, within fp32 rounding otherwise; fp16 rows round once."""
     rng = np.random.default_rng(23)
     rows, dim, bags, hot = 50, 8, 100, 10
     keys = (rng.zipf(1.5, size=bags * hot) % rows).astype(np.int64)
     g = dyadic(rng, (bags, dim))
-    a = O.pooling_backprop(keys, SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim, max_run=1)
-    b = O.pooling_backprop(keys, SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim, max_run=1 << 20)
+    a = O.pooling_backprop(keys, SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim, block=1)
+    b = O.pooling_backprop(keys, SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim, block=1 << 20)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
     g16 = rng.normal(0, 0.05, size=(bags, dim)).astype(np.float16)
     uq, out = O.pooling_backprop(keys, MEAN, O.FIXED, None, bags, hot, None, O.F16, g16.view(np.uint16),
@@ -130,3 +130,26 @@ def test_positions_outside_every_bag_add_nothing():
     got = sparse_to_dense(uq, out, rows, O.F32)
     assert set(uq.tolist()) == set(keys.tolist())  # every key is reported, some with a zero row
     assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("block", [1, 3, 8, 32, 64])
+def test_hot_keys_over_many_blocks(block):
+    """Keys whose positions span many blocks (up to hundreds of pieces, so all
+    eight sub-sequences are used and the last ones are short or empty) sum to the
+    autograd gradient: exactly for dyadic values, within fp32 rounding
+    otherwise."""
+    rng = np.random.default_rng(31 + block)
+    rows, dim, bags, hot = 40, 8, 120, 16
+    keys = np.where(rng.random(bags * hot) < 0.6, 0, rng.integers(0, rows, bags * hot)).astype(np.int64)
+    keys[:5] = 7  # a key whose few pieces leave quarters empty when block is large
+    g = dyadic(rng, (bags, dim))
+    uq, out = O.pooling_backprop(keys, SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim,
+                                 block=block)
+    ref = dense_grad_torch(keys, SUM, O.FIXED, None, bags, hot, None, g, rows)
+    assert np.array_equal(sparse_to_dense(uq, out, rows, O.F32), ref)
+    w = rng.uniform(0.1, 1.0, size=bags * hot).astype(np.float32)
+    gn = rng.normal(0, 1, size=(bags, dim)).astype(np.float32)
+    uq, out = O.pooling_backprop(keys, WMEAN, O.FIXED, None, bags, hot, w, O.F32, gn, O.F32, dim,
+                                 block=block)
+    ref = dense_grad_torch(keys, WMEAN, O.FIXED, None, bags, hot, w, gn, rows)
+    assert np.allclose(sparse_to_dense(uq, out, rows, O.F32), ref, rtol=1e-5, atol=1e-5)
