@@ -72,7 +72,7 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   NVE_HIP(key_span(b.ka, n, b.span, s));
   const unsigned long long span = read_back(b.span, s);
   int alt = 0;
-  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, (bits_for(span) + 7) / 8 * 8, b.sort_tmp,
+  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, bits_for(span), b.sort_tmp,
                            &alt, s));
   const uint64_t* ks = alt ? b.kb : b.ka;
   const uint32_t* vs = alt ? b.vb : b.va;
@@ -97,7 +97,7 @@ void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t*
   NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, s));
   int alt = 0;
   NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0,
-                           (bits_for((uint64_t)(num_rows > 1 ? num_rows - 1 : 1)) + 7) / 8 * 8,
+                           bits_for((uint64_t)(num_rows > 1 ? num_rows - 1 : 1)),
                            b.sort_tmp, &alt, s));
   GatherLaunch g{};
   g.keys = alt ? b.kb : b.ka;  // sorted keys as int64

@@ -8,16 +8,17 @@
 // Only the mathematical results matter (a stable sort; descending sorts are
 // expressed by the caller as ascending sorts of a complemented key).
 //
-// One pass per 8-bit digit, three kernels per pass:
+// One pass per digit of 8 bits, or of 9 when that takes fewer passes (the
+// last digit keeps only the bits below end_bit), three kernels per pass:
 //   hist     each 256-thread workgroup counts the digits of its 1024-key tile
-//            into LDS and writes the 256 counts digit-major;
+//            into LDS and writes the counts digit-major;
 //   rowscan  one workgroup per digit turns its row of per-tile counts into
 //            exclusive prefixes (a separate array) and writes the digit's total;
-//   scatter  each workgroup scans the 256 digit totals (digit d starts after
+//   scatter  each workgroup scans the digit totals (digit d starts after
 //            every smaller digit) and adds its tile's row prefix (digit d of
 //            tile t lands after digit d of tiles < t: this is what makes the
 //            pass stable).  It ranks its keys stably inside the tile -- a wave
-//            finds the lanes sharing its digit with eight ballots, ranks by
+//            finds the lanes sharing its digit with one ballot per digit bit, ranks by
 //            popcount of the lower lanes, and adds the counts of earlier waves
 //            and rounds -- stages the tile in LDS in digit order, and writes
 //            it out so that consecutive threads store consecutive positions of
@@ -35,21 +36,26 @@ namespace nve_amd {
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 4;
 constexpr int kSortTile = kSortThreads * kSortItems;
+constexpr int kMaxBins = 512;  // digits of at most 9 bits
 
+template <int RB>
 __global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, int64_t n, int shift,
-                                                         uint32_t* counts, int nblocks) {
-  __shared__ uint32_t h[256];
+                                                         uint32_t mask, uint32_t* counts, int nblocks) {
+  constexpr int kBins = 1 << RB;
+  __shared__ uint32_t h[kBins];
   const int tid = threadIdx.x;
-  h[tid] = 0;
+#pragma unroll
+  for (int d = tid; d < kBins; d += kSortThreads) h[d] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t i = base + r * kSortThreads + tid;
-    if (i < n) atomicAdd(&h[(keys[i] >> shift) & 255u], 1u);
+    if (i < n) atomicAdd(&h[(uint32_t)(keys[i] >> shift) & mask], 1u);
   }
   __syncthreads();
-  counts[(int64_t)tid * nblocks + blockIdx.x] = h[tid];
+#pragma unroll
+  for (int d = tid; d < kBins; d += kSortThreads) counts[(int64_t)d * nblocks + blockIdx.x] = h[d];
 }
 
 // Inclusive scan across the 64 lanes of a wave.
@@ -132,6 +138,23 @@ __global__ __launch_bounds__(256) void scan_down_kernel(uint32_t* data, int64_t 
     *total = off + block_total;
 }
 
+// Exclusive scan of the D consecutive values v[0..D) of each of the
+// workgroup's NT threads (thread t holds items t*D .. t*D+D-1), in place.
+template <int NT, int D>
+__device__ __forceinline__ void block_exclusive_scan_items(uint32_t* v, uint32_t* lds,
+                                                           uint32_t* total) {
+  uint32_t s = 0;
+#pragma unroll
+  for (int j = 0; j < D; ++j) s += v[j];
+  uint32_t run = block_exclusive_scan<NT>(s, lds, total);
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const uint32_t x = v[j];
+    v[j] = run;
+    run += x;
+  }
+}
+
 // Row d of the digit-major per-tile counts -> exclusive prefixes in offs;
 // totals[d] = the row's sum.  One workgroup per digit.
 __global__ __launch_bounds__(256) void radix_rowscan_kernel(const uint32_t* counts, uint32_t* offs,
@@ -161,17 +184,21 @@ __global__ __launch_bounds__(256) void radix_rowscan_kernel(const uint32_t* coun
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+template <int RB>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys, const uint32_t* vals,
                                                             uint64_t* ko, uint32_t* vo, int64_t n,
-                                                            int shift, const uint32_t* counts,
+                                                            int shift, uint32_t mask,
+                                                            const uint32_t* counts,
                                                             const uint32_t* offs,
                                                             const uint32_t* totals, int nblocks) {
+  constexpr int kBins = 1 << RB;
+  constexpr int D = kBins / kSortThreads;                    // digits per thread
   constexpr int kSlots = kSortItems * (kSortThreads / 64);  // (round, wave) pairs in key order
   __shared__ uint64_t sk[kSortTile];
   __shared__ uint32_t sv[kSortTile];
-  __shared__ uint32_t lstart[256];          // first local position of digit d in the tile
-  __shared__ uint32_t gbase[256];           // output position of that key
-  __shared__ uint32_t slot[kSlots][256];    // keys of digit d per (round, wave), then their prefix
+  __shared__ uint32_t lstart[kBins];          // first local position of digit d in the tile
+  __shared__ uint32_t gbase[kBins];           // output position of that key
+  __shared__ uint32_t slot[kSlots][kBins];    // keys of digit d per (round, wave), then their prefix
   __shared__ uint32_t lds[256 / 64 + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -187,14 +214,25 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
     k[r] = li < tile_n ? keys[base + li] : 0ull;
     v[r] = li < tile_n ? vals[base + li] : 0u;
   }
-  const int64_t tile = (int64_t)tid * nblocks + blockIdx.x;
-  uint32_t all;
-  const uint32_t digit_base = block_exclusive_scan<256>(totals[tid], lds, &all);
-  const uint32_t local = block_exclusive_scan<256>(counts[tile], lds, &all);
-  lstart[tid] = local;
-  gbase[tid] = digit_base + offs[tile];
+  // thread t owns digits t*D .. t*D+D-1
+  uint32_t dbase[D], loc[D];
 #pragma unroll
-  for (int q = 0; q < kSlots; ++q) slot[q][tid] = 0;
+  for (int j = 0; j < D; ++j) {
+    const int d = tid * D + j;
+    dbase[j] = totals[d];
+    loc[j] = counts[(int64_t)d * nblocks + blockIdx.x];
+  }
+  uint32_t all;
+  block_exclusive_scan_items<kSortThreads, D>(dbase, lds, &all);
+  block_exclusive_scan_items<kSortThreads, D>(loc, lds, &all);
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int d = tid * D + j;
+    lstart[d] = loc[j];
+    gbase[d] = dbase[j] + offs[(int64_t)d * nblocks + blockIdx.x];
+#pragma unroll
+    for (int q = 0; q < kSlots; ++q) slot[q][d] = 0;
+  }
   __syncthreads();
   // per (round, wave): lanes sharing the digit, rank among them, count by the leader
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -202,10 +240,10 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const bool valid = r * kSortThreads + tid < tile_n;
-    const uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
+    const uint32_t d = (uint32_t)(k[r] >> shift) & mask;
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < RB; ++b) {
       const uint64_t m = __ballot((d >> b) & 1u);
       peers &= ((d >> b) & 1u) ? m : ~m;
     }
@@ -213,13 +251,15 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
     if (valid && rank[r] == 0) slot[r * (kSortThreads / 64) + wave][d] = (uint32_t)__popcll(peers);
   }
   __syncthreads();
-  // thread d: exclusive prefix of digit d over the slots, from its local start
-  {
-    uint32_t acc = lstart[tid];
+  // digit d: exclusive prefix over the slots, from its local start
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int d = tid * D + j;
+    uint32_t acc = lstart[d];
 #pragma unroll
     for (int q = 0; q < kSlots; ++q) {
-      const uint32_t c = slot[q][tid];
-      slot[q][tid] = acc;
+      const uint32_t c = slot[q][d];
+      slot[q][d] = acc;
       acc += c;
     }
   }
@@ -227,7 +267,7 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     if (r * kSortThreads + tid < tile_n) {
-      const uint32_t d = (uint32_t)(k[r] >> shift) & 255u;
+      const uint32_t d = (uint32_t)(k[r] >> shift) & mask;
       const uint32_t pos = slot[r * (kSortThreads / 64) + wave][d] + rank[r];
       sk[pos] = k[r];
       sv[pos] = v[r];
@@ -237,7 +277,7 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
   // the tile in digit order: runs of one digit go to consecutive positions
   for (int j = tid; j < tile_n; j += kSortThreads) {
     const uint64_t kk = sk[j];
-    const uint32_t d = (uint32_t)(kk >> shift) & 255u;
+    const uint32_t d = (uint32_t)(kk >> shift) & mask;
     const uint32_t pos = gbase[d] + (uint32_t)j - lstart[d];
     ko[pos] = kk;
     vo[pos] = sv[j];
@@ -277,7 +317,8 @@ size_t scan_temp_bytes(int64_t m) {
 
 size_t radix_sort_temp_bytes(int64_t n) {
   const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
-  const size_t sort = (size_t)(nblocks > 0 ? nblocks : 1) * 256 * sizeof(uint32_t) * 2 + 1024;
+  const size_t sort = (size_t)(nblocks > 0 ? nblocks : 1) * kMaxBins * sizeof(uint32_t) * 2 +
+                      kMaxBins * sizeof(uint32_t) + 1024;
   const size_t scan = scan_temp_bytes(n);
   return sort > scan ? sort : scan;
 }
@@ -290,19 +331,34 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
   if (nblocks > 0x7fffffff) return hipErrorInvalidValue;
   uint32_t* counts = static_cast<uint32_t*>(temp);
-  uint32_t* offs = counts + nblocks * 256;
-  uint32_t* totals = offs + nblocks * 256;
+  uint32_t* offs = counts + nblocks * kMaxBins;
+  uint32_t* totals = offs + nblocks * kMaxBins;
   uint64_t* ki = keys;
   uint32_t* vi = vals;
   uint64_t* ka = keys_alt;
   uint32_t* va = vals_alt;
-  for (int shift = begin_bit; shift < end_bit; shift += 8) {
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
-                       shift, counts, (int)nblocks);
-    hipLaunchKernelGGL(radix_rowscan_kernel, dim3(256), dim3(256), 0, stream, counts, offs,
-                       (int)nblocks, totals);
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, vi,
-                       ka, va, n, shift, counts, offs, totals, (int)nblocks);
+  // 9-bit digits when they take fewer passes than 8-bit ones (26-bit keys: 3
+  // passes instead of 4); the last digit keeps only the bits below end_bit
+  const int width = end_bit - begin_bit;
+  const int rb = (width + 8) / 9 < (width + 7) / 8 ? 9 : 8;
+  for (int shift = begin_bit; shift < end_bit; shift += rb) {
+    const int bits = end_bit - shift < rb ? end_bit - shift : rb;
+    const uint32_t mask = (1u << bits) - 1u;
+    if (rb == 9) {
+      hipLaunchKernelGGL(radix_hist_kernel<9>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
+                         shift, mask, counts, (int)nblocks);
+      hipLaunchKernelGGL(radix_rowscan_kernel, dim3(1u << 9), dim3(256), 0, stream, counts, offs,
+                         (int)nblocks, totals);
+      hipLaunchKernelGGL(radix_scatter_kernel<9>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki,
+                         vi, ka, va, n, shift, mask, counts, offs, totals, (int)nblocks);
+    } else {
+      hipLaunchKernelGGL(radix_hist_kernel<8>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
+                         shift, mask, counts, (int)nblocks);
+      hipLaunchKernelGGL(radix_rowscan_kernel, dim3(1u << 8), dim3(256), 0, stream, counts, offs,
+                         (int)nblocks, totals);
+      hipLaunchKernelGGL(radix_scatter_kernel<8>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki,
+                         vi, ka, va, n, shift, mask, counts, offs, totals, (int)nblocks);
+    }
     std::swap(ki, ka);
     std::swap(vi, va);
     *result_in_alt ^= 1;

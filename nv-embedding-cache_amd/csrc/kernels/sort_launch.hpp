@@ -15,7 +15,7 @@ size_t radix_sort_temp_bytes(int64_t n);
 size_t scan_temp_bytes(int64_t m);
 
 // Stable ascending sort of (keys[i], vals[i]) on bits [begin_bit, end_bit) of
-// the keys (begin_bit a multiple of 8).  Ping-pongs between (keys, vals) and
+// the keys (digits of 8 or 9 bits from begin_bit).  Ping-pongs between (keys, vals) and
 // (keys_alt, vals_alt); *result_in_alt says which pair holds the result.
 hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                             int64_t n, int begin_bit, int end_bit, void* temp, int* result_in_alt,

@@ -33,7 +33,6 @@ int bits_for(uint64_t max_value) {
   return b;
 }
 
-int round8(int bits) { return (bits + 7) / 8 * 8; }
 
 template <typename T>
 T* carve(uint8_t*& p, size_t count) {
@@ -133,7 +132,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   NVE_HIP(key_span(ka, n, d_span, s));
   const unsigned long long span = read_back(d_span, s);
   int alt = 0;
-  NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, round8(bits_for(span)), sort_tmp, &alt, s));
+  NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, bits_for(span), sort_tmp, &alt, s));
   uint64_t* ks = alt ? kb : ka;
   uint32_t* vs = alt ? vb : va;
   NVE_HIP(launch_run_heads(ks, n, heads, s));
@@ -147,7 +146,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   uint32_t* v2b = reinterpret_cast<uint32_t*>(rset);
   NVE_HIP(launch_count_key(start, uniq, k2, v2, s));
   int alt2 = 0;
-  NVE_HIP(radix_sort_pairs(k2, v2, k2b, v2b, uniq, 0, round8(bits_for((uint64_t)n)), sort_tmp, &alt2, s));
+  NVE_HIP(radix_sort_pairs(k2, v2, k2b, v2b, uniq, 0, bits_for((uint64_t)n), sort_tmp, &alt2, s));
   const uint32_t* order = alt2 ? v2b : v2;
   const uint32_t m = (uint32_t)std::min<int64_t>(uniq, cfg_.max_modify_size);
   // hist entries and their sets (k3 / v3 reuse the first sort's free buffers)
@@ -160,7 +159,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   uint64_t* k3b = reinterpret_cast<uint64_t*>(ukey);  // runs' keys are consumed by now
   uint32_t* v3b = heads;
   int alt3 = 0;
-  NVE_HIP(radix_sort_pairs(k3, v3, k3b, v3b, m, 0, round8(bits_for(num_sets_ - 1)), sort_tmp, &alt3, s));
+  NVE_HIP(radix_sort_pairs(k3, v3, k3b, v3b, m, 0, bits_for(num_sets_ - 1), sort_tmp, &alt3, s));
   const uint64_t* sk = alt3 ? k3b : k3;
   const uint32_t* sv = alt3 ? v3b : v3;
   NVE_HIP(launch_run_heads(sk, m, start, s));  // start reused as head flags

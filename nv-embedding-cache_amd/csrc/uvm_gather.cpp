@@ -56,7 +56,7 @@ SortedLookups sort_lookups(ExecutionContext& ctx, const GatherLaunch& g, int key
                            uint64_t uvm_rows, bool want_misses, hipStream_t s) {
   const int64_t n = g.n;
   const int bits = std::max(1, std::min(62, bits_for(uvm_rows)));
-  const int end_bit = (bits + 1 + 7) / 8 * 8;
+  const int end_bit = bits + 1;
   const size_t bytes = 256 * 8 + (size_t)n * (8 * 2 + 4 * 2 + 8) + radix_sort_temp_bytes(n);
   uint8_t* p = static_cast<uint8_t*>(ctx.buffer("sort_gather", bytes));
   unsigned long long* nmiss = carve<unsigned long long>(p, 1);
