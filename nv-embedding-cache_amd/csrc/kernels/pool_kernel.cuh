@@ -256,13 +256,22 @@ inline int pool_log2(int x) {
 }
 
 // Launches pool_kernel<S, V, U, W> for the geometry's unroll and the launch's
-// weighting.
+// weighting.  Row formats with per-row metadata (scale / offset) keep fewer
+// rows in flight (8, or 4 when a lane decodes 16 elements): the kernel is
+// built for 1024-thread workgroups, 128 registers per lane, and with more
+// rows their decode state would go to scratch memory.
 template <int S, int V>
 hipError_t launch_pool_sv(const PoolLaunch& a, const PoolGeometry& g, hipStream_t stream) {
   const int gs = pool_log2(g.g);
   const int ps = pool_log2(g.gpb);
   const dim3 grid((unsigned)g.grid), block((unsigned)g.threads);
-  if (g.unroll == 16) {
+  if constexpr (Fmt<S>::meta != 0) {
+    constexpr int kU = V / Fmt<S>::esize >= 16 ? 4 : 8;
+    if (a.weighted)
+      hipLaunchKernelGGL((pool_kernel<S, V, kU, true>), grid, block, g.lds_bytes, stream, a, gs, ps, g.passes);
+    else
+      hipLaunchKernelGGL((pool_kernel<S, V, kU, false>), grid, block, g.lds_bytes, stream, a, gs, ps, g.passes);
+  } else if (g.unroll == 16) {
     if (a.weighted)
       hipLaunchKernelGGL((pool_kernel<S, V, 16, true>), grid, block, g.lds_bytes, stream, a, gs, ps, g.passes);
     else
