@@ -300,6 +300,17 @@ def run_workload(args, torch, _lib):
         layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
         _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), table, None)
         _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
+        if args.c3_prefill:
+            # every row of the backing table into the cache first (the table must fit it), so
+            # that the lookups measure the cache-hit path alone
+            tctx = ctypes.c_void_p()
+            _lib.call("nve_table_create_execution_context", table, ctypes.byref(tctx), sp, sp, None, None)
+            step = 1 << 20
+            for r0 in range(0, rows, step):
+                ks = torch.arange(r0, min(rows, r0 + step), dtype=torch.int64, device="cuda")
+                _lib.call("nve_amd_table_insert_from_uvm", table, tctx, ks.numel(), ctypes.c_void_p(ks.data_ptr()))
+                _lib.call("nve_context_wait", tctx)
+            _lib.call("nve_context_destroy", tctx)
         concat = args.c3_concat
         out = torch.empty((nkeys if concat else bags, dim), dtype=torch.float16, device="cuda")
         hr = (ctypes.c_float * 1)()
@@ -345,7 +356,7 @@ def run_workload(args, torch, _lib):
                         "zipf_alpha": alpha, "mean_hit_rate": round(hit, 4),
                         "host_link_bytes_per_step": int(nkeys * (1 - hit)) * width,
                         "lookup": "concat" if concat else f"pooled {bags} x {hot} Sum",
-                        "kernel_mode": args.kernel_mode,
+                        "kernel_mode": args.kernel_mode, "prefilled": bool(args.c3_prefill),
                         "step": "lookup + hit-rate readback + auto-insert when the heuristic fires"})
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
@@ -476,6 +487,8 @@ def main():
     ap.add_argument("--c3-rows", type=int, default=256_000_000, help="c3: host table rows")
     ap.add_argument("--c3-cache-gib", type=int, default=20, help="c3: GPU cache size in GiB")
     ap.add_argument("--c3-concat", action="store_true", help="c3: one row per key instead of pooled bags")
+    ap.add_argument("--c3-prefill", action="store_true",
+                    help="c3: insert every backing row into the cache before the lookups (hit path only)")
     ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],
                     help="c3: GPU table lookup mode (0 auto, 1 LookupUVM, 2 SortGather, 3 PipelineGather)")
     ap.add_argument("--no-cpu", action="store_true")
