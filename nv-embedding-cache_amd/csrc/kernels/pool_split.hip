@@ -95,8 +95,58 @@ struct SplitArgs {
   int gpb_shift;
 };
 
-template <int SDT, int G, bool W>
-__global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
+// Long bags over a set-associative cache (with or without a backing table):
+// the split kernel's arguments plus the cache.
+struct SplitCacheArgs : SplitArgs {
+  const uint8_t* cache_data;
+  const void* cache_tags;
+  uint64_t num_sets;
+  unsigned long long* miss_counter;  // optional
+};
+
+constexpr uint32_t kBackingRow = 0x80000000u;  // code bit: a backing-table row, not a cache slot
+
+// The 32-bit code of a key's row in a cache-backed table: the cache slot
+// set * 8 + way on a hit (the lowest way whose rebuilt key tag * num_sets + set
+// equals the key, as resolve_row), else kBackingRow | key when the backing
+// table holds the key, else kNoRow.  *miss reports a cache miss.
+__device__ __forceinline__ uint32_t cache_code(const SplitCacheArgs& a, int64_t key, bool* miss) {
+  uint32_t set, mask = 0;
+  if (a.key_bytes == 4) {
+    const uint32_t uk = (uint32_t)(int32_t)key;
+    const uint32_t ns = (uint32_t)a.num_sets;
+    set = uk % ns;
+    const uint4* tp = reinterpret_cast<const uint4*>(reinterpret_cast<const int32_t*>(a.cache_tags) +
+                                                     (uint64_t)set * 8);
+    const uint4 t0 = tp[0];
+    const uint4 t1 = tp[1];
+    const uint32_t t[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * ns + set == uk) << w;
+  } else {
+    const uint64_t uk = (uint64_t)key;
+    set = (uint32_t)(uk % a.num_sets);
+    const uint4* tp = reinterpret_cast<const uint4*>(reinterpret_cast<const int64_t*>(a.cache_tags) +
+                                                     (uint64_t)set * 8);
+    uint64_t t[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 q = tp[c];
+      t[2 * c] = (uint64_t)q.x | ((uint64_t)q.y << 32);
+      t[2 * c + 1] = (uint64_t)q.z | ((uint64_t)q.w << 32);
+    }
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * a.num_sets + set == uk) << w;
+  }
+  *miss = mask == 0;
+  if (mask) return set * 8u + (uint32_t)__builtin_ctz(mask);
+  if (a.table != nullptr && (uint64_t)key < a.num_rows) return kBackingRow | (uint32_t)key;
+  return kNoRow;
+}
+
+template <int SDT, int G, bool W, bool CACHE = false>
+__global__ __launch_bounds__(1024) void pool_split_kernel(
+    std::conditional_t<CACHE, SplitCacheArgs, SplitArgs> a) {
   constexpr int VB = 16;
   constexpr int ES = Fmt<SDT>::esize;
   constexpr int E = VB / ES;
@@ -142,13 +192,20 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
   float wsum = 0.0f;
 
   const int lane = tid & 63;
+  uint32_t misses = 0;
   for (int64_t k0 = cs; k0 < ce; k0 += G) {
     const int64_t kk = k0 + gl;
     uint32_t ridx = kNoRow;
     float w = 0.0f;
     if (kk < ce) {
       const int64_t key = load_key(a.keys, a.key_bytes, kk);
-      if ((uint64_t)key < num_rows) ridx = (uint32_t)key;  // keys outside the table read nothing
+      if constexpr (CACHE) {
+        bool miss;
+        ridx = cache_code(a, key, &miss);
+        misses += miss ? 1u : 0u;
+      } else {
+        if ((uint64_t)key < num_rows) ridx = (uint32_t)key;  // keys outside the table read nothing
+      }
       if (W) w = load_weight(a.weights, a.weight_dtype, kk);
     }
     const int n = (int)((ce - k0) < G ? (ce - k0) : G);
@@ -165,8 +222,14 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool real = ri[u] != kNoRow && in_row;
-        const uint64_t addr = real ? table + (uint64_t)ri[u] * row_bytes + (uint64_t)off
-                                   : zero_row + (uint64_t)(off & kZeroRowMask);
+        uint64_t base;
+        if constexpr (CACHE) {
+          base = (ri[u] & kBackingRow) ? table + (uint64_t)(ri[u] & ~kBackingRow) * row_bytes
+                                       : (uint64_t)a.cache_data + (uint64_t)ri[u] * row_bytes;
+        } else {
+          base = table + (uint64_t)ri[u] * row_bytes;
+        }
+        const uint64_t addr = real ? base + (uint64_t)off : zero_row + (uint64_t)(off & kZeroRowMask);
         v[u] = load_vec<VB>(addr);
       }
 #pragma unroll
@@ -189,6 +252,21 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(SplitArgs a) {
 
   // butterfly over the wave's groups (the same pairing and additions as pool_kernel)
   butterfly<G>(acc, E, wsum, W);
+  if constexpr (CACHE) {
+    // one miss-counter atomic per workgroup: thousands on one address serialize
+    if (a.miss_counter != nullptr) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) misses += __shfl_xor(misses, o);
+      __shared__ uint32_t wave_misses[16];
+      if (lane == 0) wave_misses[tid >> 6] = misses;
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t m = 0;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m += wave_misses[w];
+        if (m) atomicAdd(a.miss_counter, (unsigned long long)m);
+      }
+    }
+  }
 
   // waves' partial rows, added in wave order
   constexpr int row_elems = G * E;
@@ -252,6 +330,19 @@ hipError_t launch_split_g(const PoolLaunch& a, const PoolGeometry& g, hipStream_
   s.gpb_shift = 0;
   while ((1 << s.gpb_shift) < g.gpb) ++s.gpb_shift;
   const dim3 grid((unsigned)g.grid), block((unsigned)g.threads);
+  if (a.src.cache_data != nullptr) {
+    SplitCacheArgs c{};
+    static_cast<SplitArgs&>(c) = s;
+    c.cache_data = a.src.cache_data;
+    c.cache_tags = a.src.cache_tags;
+    c.num_sets = a.src.num_sets;
+    c.miss_counter = a.miss_counter;
+    if (a.weighted)
+      hipLaunchKernelGGL((pool_split_kernel<SDT, G, true, true>), grid, block, g.lds_bytes, stream, c);
+    else
+      hipLaunchKernelGGL((pool_split_kernel<SDT, G, false, true>), grid, block, g.lds_bytes, stream, c);
+    return hipGetLastError();
+  }
   if (a.weighted)
     hipLaunchKernelGGL((pool_split_kernel<SDT, G, true>), grid, block, g.lds_bytes, stream, s);
   else
@@ -489,8 +580,15 @@ hipError_t launch_pool_short(const PoolLaunch& a, const PoolGeometry& g, hipStre
 }
 
 bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g) {
-  if (a.src.cache_data != nullptr || a.num_tables > 0 || !a.src.load_indices) return false;
-  if (a.src.table == nullptr || a.src.num_rows == 0 || a.src.num_rows >= kNoRow) return false;
+  if (a.num_tables > 0 || !a.src.load_indices) return false;
+  if (a.src.cache_data != nullptr) {
+    // 32-bit row codes: cache slots and backing rows below 2^31
+    if (a.src.num_sets == 0 || a.src.num_sets * 8 >= kBackingRow) return false;
+    if (a.src.table != nullptr && (a.src.num_rows == 0 || a.src.num_rows >= kBackingRow)) return false;
+    if (a.key_bytes == 4 && a.src.num_sets > 0xffffffffull) return false;
+  } else if (a.src.table == nullptr || a.src.num_rows == 0 || a.src.num_rows >= kNoRow) {
+    return false;
+  }
   if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
   if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;
   if (g.vb != 16 || g.passes != 1 || g.bags_per_wg != 1) return false;
