@@ -313,11 +313,18 @@ constexpr int kZeroRowBytes = 4096;
 constexpr int64_t kZeroRowMask = kZeroRowBytes - 1;
 static __device__ __align__(16) uint8_t g_zero_row[kZeroRowBytes + 64] = {};
 
-// Adds the wave's per-lane miss counts to *counter (every lane active).
+// Miss counters are kMissStripes words; a workgroup adds to word
+// blockIdx.x % kMissStripes and readers add the words up: thousands of
+// atomics on one address serialize in one memory channel.
+constexpr int kMissStripes = 8;
+
+// Adds the wave's per-lane miss counts to the workgroup's counter word (every
+// lane active).
 __device__ __forceinline__ void add_misses(unsigned long long* counter, uint32_t n) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
-  if (__lane_id() == 0 && n) atomicAdd(counter, (unsigned long long)n);
+  if (__lane_id() == 0 && n)
+    atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)n);
 }
 
 // ---------------------------------------------------------------------------

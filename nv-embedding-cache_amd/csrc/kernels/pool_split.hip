@@ -101,7 +101,7 @@ struct SplitCacheArgs : SplitArgs {
   const uint8_t* cache_data;
   const void* cache_tags;
   uint64_t num_sets;
-  unsigned long long* miss_counter;  // optional
+  unsigned long long* miss_counter;  // optional, kMissStripes words
 };
 
 constexpr uint32_t kBackingRow = 0x80000000u;  // code bit: a backing-table row, not a cache slot
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(
       if (tid == 0) {
         uint32_t m = 0;
         for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m += wave_misses[w];
-        if (m) atomicAdd(a.miss_counter, (unsigned long long)m);
+        if (m) atomicAdd(a.miss_counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)m);
       }
     }
   }

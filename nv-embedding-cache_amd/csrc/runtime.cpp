@@ -190,19 +190,27 @@ void* ExecutionContext::buffer(const std::string& name, size_t bytes, bool host)
 
 unsigned long long* ExecutionContext::miss_counter() {
   if (!misses_) {
-    NVE_HIP(hipMalloc(&misses_, sizeof(unsigned long long)));
-    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(misses_), 1, 0, lookup_));
+    NVE_HIP(hipMalloc(&misses_, kMissCounterWords * sizeof(unsigned long long)));
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(misses_), kMissCounterWords, 0, lookup_));
   }
   return misses_;
 }
 
 void ExecutionContext::reset_misses() {
   // a fill kernel rather than a memset node, so the lookup stays capturable
-  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(miss_counter()), 1, 0, lookup_));
+  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(miss_counter()), kMissCounterWords, 0, lookup_));
 }
 
 int64_t ExecutionContext::read_misses() {
-  return (int64_t)read_back(miss_counter(), lookup_);
+  return read_miss_words(miss_counter(), lookup_);
+}
+
+int64_t read_miss_words(const unsigned long long* counter, hipStream_t stream) {
+  unsigned long long w[kMissCounterWords];
+  read_small(w, counter, sizeof(w), stream);
+  unsigned long long t = 0;
+  for (int i = 0; i < kMissCounterWords; ++i) t += w[i];
+  return (int64_t)t;
 }
 
 void ExecutionContext::add_pending(std::future<void> f) {

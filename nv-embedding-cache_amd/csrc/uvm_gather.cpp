@@ -59,14 +59,14 @@ SortedLookups sort_lookups(ExecutionContext& ctx, const GatherLaunch& g, int key
   const int end_bit = bits + 1;
   const size_t bytes = 256 * 8 + (size_t)n * (8 * 2 + 4 * 2 + 8) + radix_sort_temp_bytes(n);
   uint8_t* p = static_cast<uint8_t*>(ctx.buffer("sort_gather", bytes));
-  unsigned long long* nmiss = carve<unsigned long long>(p, 1);
+  unsigned long long* nmiss = carve<unsigned long long>(p, kMissCounterWords);
   uint64_t* ka = carve<uint64_t>(p, (size_t)n);
   uint64_t* kb = carve<uint64_t>(p, (size_t)n);
   uint32_t* va = carve<uint32_t>(p, (size_t)n);
   uint32_t* vb = carve<uint32_t>(p, (size_t)n);
   uint8_t* sorted_keys = carve<uint8_t>(p, (size_t)n * 8);
   void* tmp = p;
-  if (want_misses) NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(nmiss), 1, 0, s));
+  if (want_misses) NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(nmiss), kMissCounterWords, 0, s));
   NVE_HIP(launch_sortgather_keys(g.keys, n, key_bytes, g.src, bits, ka, va, g.miss_counter,
                                  want_misses ? nmiss : nullptr, s));
   int alt = 0;
@@ -75,7 +75,7 @@ SortedLookups sort_lookups(ExecutionContext& ctx, const GatherLaunch& g, int key
   NVE_HIP(launch_permute_keys(g.keys, key_bytes, pos, n, sorted_keys, s));
   SortedLookups r{pos, sorted_keys, 0};
   if (want_misses) {
-    r.misses = (uint32_t)read_back(nmiss, s);
+    r.misses = (uint32_t)read_miss_words(nmiss, s);
   }
   return r;
 }
