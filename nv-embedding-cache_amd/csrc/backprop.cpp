@@ -25,6 +25,7 @@
 #include "kernels/launch.hpp"
 #include "kernels/sort_launch.hpp"
 #include "layers.hpp"
+#include "runtime.hpp"
 
 namespace nve_amd {
 
@@ -116,8 +117,10 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
   BackpropBufs b = carve(ws, n, num_bags);
 
   // (1) dedup: unique keys straight into the caller's buffer
-  const int64_t u = dedup_run(key_bytes, n, keys, unique_out, b.counts, b.inverse, b.doff, b.dedup_ws,
-                              b.dedup_bytes, s, b.kidx);
+  // (the unique count is read once everything is queued: no stall in between)
+  const uint32_t* u_dev = nullptr;
+  dedup_run(key_bytes, n, keys, unique_out, b.counts, b.inverse, b.doff, b.dedup_ws, b.dedup_bytes, s,
+            b.kidx, &u_dev);
 
   // (2) gradient row and weight per dedup position
   if (mode == kBackpropMean || mode == kBackpropWMean)
@@ -144,7 +147,7 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
   const int weighted = (mode == kBackpropWSum || mode == kBackpropMean || mode == kBackpropWMean) ? 1 : 0;
   NVE_HIP(launch_piece_pool(a, f16, weighted, s));
   NVE_HIP(launch_piece_combine(a, f16, s));
-  return u;
+  return (int64_t)read_back(u_dev, s);
 }
 
 }  // namespace nve_amd

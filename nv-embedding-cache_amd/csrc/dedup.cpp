@@ -62,7 +62,7 @@ size_t dedup_workspace_bytes(int64_t n) {
 
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
                   void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
-                  uint32_t* pos_key) {
+                  uint32_t* pos_key, const uint32_t** count_dev) {
   if (n <= 0) return 0;
   NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
   NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
@@ -80,8 +80,13 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, b.sort_tmp, s));
   NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start,
                                pos_key, s));
+  if (count_dev != nullptr) {  // the caller reads the count when it needs it
+    NVE_HIP(launch_dedup_counts(b.start, (uint32_t)n, b.total, key_bytes, counts, s));
+    *count_dev = b.total;
+    return -1;
+  }
   const uint32_t u = read_back(b.total, s);
-  NVE_HIP(launch_dedup_counts(b.start, u, key_bytes, counts, s));
+  NVE_HIP(launch_dedup_counts(b.start, u, nullptr, key_bytes, counts, s));
   return (int64_t)u;
 }
 

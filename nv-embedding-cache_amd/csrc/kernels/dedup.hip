@@ -42,10 +42,14 @@ __global__ __launch_bounds__(256) void dedup_outputs_kernel(const uint64_t* ks, 
   if (i == n - 1) start[scan[i] + (head ? 1u : 0u)] = (uint32_t)n;
 }
 
+// u_dev (optional): the unique count in device memory, for a grid sized by an
+// upper bound without reading the count back first.
 __global__ __launch_bounds__(256) void dedup_counts_kernel(const uint32_t* start, uint32_t u_n,
-                                                           int key_bytes, void* counts) {
+                                                           const uint32_t* u_dev, int key_bytes,
+                                                           void* counts) {
   const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
-  if (u < u_n) store_key(counts, key_bytes, u, (int64_t)(start[u + 1] - start[u]));
+  const uint32_t m = u_dev != nullptr ? *u_dev : u_n;
+  if (u < m) store_key(counts, key_bytes, u, (int64_t)(start[u + 1] - start[u]));
 }
 
 hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int flip, uint64_t* k64,
@@ -66,11 +70,11 @@ hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const ui
   return hipGetLastError();
 }
 
-hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, int key_bytes, void* counts,
-                               hipStream_t stream) {
+hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, const uint32_t* u_dev,
+                               int key_bytes, void* counts, hipStream_t stream) {
   if (u_n == 0) return hipSuccess;
   hipLaunchKernelGGL(dedup_counts_kernel, dim3((u_n + 255) / 256), dim3(256), 0, stream, start, u_n,
-                     key_bytes, counts);
+                     u_dev, key_bytes, counts);
   return hipGetLastError();
 }
 

@@ -13,7 +13,8 @@ hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const ui
                                 int64_t n, int key_bytes, void* unique, void* inverse,
                                 void* offsets, uint32_t* start, uint32_t* pos_key,
                                 hipStream_t stream);
-hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, int key_bytes, void* counts,
-                               hipStream_t stream);
+// counts[u] for u < u_n, or for u < *u_dev when u_dev is given (u_n an upper bound).
+hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, const uint32_t* u_dev,
+                               int key_bytes, void* counts, hipStream_t stream);
 
 }  // namespace nve_amd
