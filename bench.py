@@ -250,7 +250,9 @@ def run_workload(args, torch, _lib):
         # LinearUVM: pinned host table + 32 GiB 8-way HBM cache, warmed by 10
         # batches (auto-insert), then timed pooled lookups whose misses read the
         # host table and are inserted when the heuristic asks for it
-        rows, dim, bags, hot, alpha = args.c3_rows, 128, 256, 1024, 1.2
+        rows, dim, alpha = args.c3_rows, 128, 1.2
+        hot = args.c3_hotness
+        bags = 262144 // hot
         nkeys = bags * hot
         width = dim * 2
         log(f"c3: pinned host table {rows} x {width} B ({rows * width / 1e9:.1f} GB)")
@@ -487,6 +489,8 @@ def main():
     ap.add_argument("--c3-rows", type=int, default=256_000_000, help="c3: host table rows")
     ap.add_argument("--c3-cache-gib", type=int, default=20, help="c3: GPU cache size in GiB")
     ap.add_argument("--c3-concat", action="store_true", help="c3: one row per key instead of pooled bags")
+    ap.add_argument("--c3-hotness", type=int, default=1024, choices=[16, 32, 64, 128, 256, 512, 1024],
+                    help="c3: keys per pooled bag (262,144 keys per batch in 262,144 / hotness bags)")
     ap.add_argument("--c3-prefill", action="store_true",
                     help="c3: insert every backing row into the cache before the lookups (hit path only)")
     ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],

@@ -110,7 +110,8 @@ constexpr uint32_t kBackingRow = 0x80000000u;  // code bit: a backing-table row,
 // set * 8 + way on a hit (the lowest way whose rebuilt key tag * num_sets + set
 // equals the key, as resolve_row), else kBackingRow | key when the backing
 // table holds the key, else kNoRow.  *miss reports a cache miss.
-__device__ __forceinline__ uint32_t cache_code(const SplitCacheArgs& a, int64_t key, bool* miss) {
+template <typename A>
+__device__ __forceinline__ uint32_t cache_code(const A& a, int64_t key, bool* miss) {
   uint32_t set, mask = 0;
   if (a.key_bytes == 4) {
     const uint32_t uk = (uint32_t)(int32_t)key;
@@ -142,6 +143,21 @@ __device__ __forceinline__ uint32_t cache_code(const SplitCacheArgs& a, int64_t 
   if (mask) return set * 8u + (uint32_t)__builtin_ctz(mask);
   if (a.table != nullptr && (uint64_t)key < a.num_rows) return kBackingRow | (uint32_t)key;
   return kNoRow;
+}
+
+// Adds the workgroup's per-lane miss counts to its word of the striped miss
+// counter with one atomic (every thread of the workgroup calls it).
+__device__ __forceinline__ void add_group_misses(unsigned long long* counter, uint32_t misses) {
+  __shared__ uint32_t wave_misses[16];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) misses += __shfl_xor(misses, o);
+  if ((threadIdx.x & 63) == 0) wave_misses[threadIdx.x >> 6] = misses;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t m = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m += wave_misses[w];
+    if (m) atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)m);
+  }
 }
 
 template <int SDT, int G, bool W, bool CACHE = false>
@@ -254,18 +270,7 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(
   butterfly<G>(acc, E, wsum, W);
   if constexpr (CACHE) {
     // one miss-counter atomic per workgroup: thousands on one address serialize
-    if (a.miss_counter != nullptr) {
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) misses += __shfl_xor(misses, o);
-      __shared__ uint32_t wave_misses[16];
-      if (lane == 0) wave_misses[tid >> 6] = misses;
-      __syncthreads();
-      if (tid == 0) {
-        uint32_t m = 0;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m += wave_misses[w];
-        if (m) atomicAdd(a.miss_counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)m);
-      }
-    }
+    if (a.miss_counter != nullptr) add_group_misses(a.miss_counter, misses);
   }
 
   // waves' partial rows, added in wave order
@@ -394,8 +399,7 @@ struct ShortArgsMT : ShortArgs {
 };
 
 template <int SDT, int G, bool W, bool MT, int UMAX>
-__global__ __launch_bounds__(256) void pool_short_kernel(
-    typename std::conditional<MT, ShortArgsMT, ShortArgs>::type a) {
+__global__ __launch_bounds__(256) void pool_short_kernel(std::conditional_t<MT, ShortArgsMT, ShortArgs> a) {
   constexpr int VB = 16;
   constexpr int ES = Fmt<SDT>::esize;
   constexpr int E = VB / ES;
@@ -495,7 +499,7 @@ __global__ __launch_bounds__(256) void pool_short_kernel(
 
 template <int SDT, int G, bool MT>
 hipError_t launch_short_g(const PoolLaunch& a, hipStream_t stream) {
-  typename std::conditional<MT, ShortArgsMT, ShortArgs>::type s{};
+  std::conditional_t<MT, ShortArgsMT, ShortArgs> s{};
   s.keys = a.keys;
   s.offsets = a.offsets;
   s.weights = a.weights;
@@ -557,6 +561,8 @@ hipError_t launch_short_sdt(const PoolLaunch& a, const PoolGeometry& g, hipStrea
 }  // namespace
 
 bool pool_short_eligible(const PoolLaunch& a, const PoolGeometry& g) {
+  // short bags over a cache stay on pool_kernel: measured as fast (12.8 us for
+  // 8192 bags of 32 keys, all hits) as a cache variant of this kernel
   if (a.src.cache_data != nullptr || !a.src.load_indices) return false;
   if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
   if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;

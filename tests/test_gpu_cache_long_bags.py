@@ -1,7 +1,8 @@
-"""GPU parity of long-bag pooling over a set-associative cache (the cache
+"""GPU parity of pooling over a set-associative cache, long bags (the cache
 variant of the split kernel: cache slots and backing-table rows as 32-bit
-codes; find_and_combine over a GpuTable, find_and_combine_kernel.cuh:40-154,
-reached through a LinearUVM layer, linear_embedding_layer.cu:91-209).
+codes) and short bags (the general pool kernel); find_and_combine over a
+GpuTable, find_and_combine_kernel.cuh:40-154, reached through a LinearUVM
+layer, linear_embedding_layer.cu:91-209.
 
 * With the cache holding exact copies of backing rows, a pooled lookup must
   equal the same lookup over the linear table bit for bit (same bag cut, same
@@ -66,12 +67,14 @@ def close(layer, lctx, ct):
     ct.close()
 
 
+@pytest.mark.parametrize("shape", [(48, 600), (1500, 24)], ids=["long", "short"])
 @pytest.mark.parametrize("key_bytes", [4, 8])
 @pytest.mark.parametrize("dtype", [O.F16, O.F32])
 @pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WSUM])
-def test_cached_copies_equal_the_linear_table_bitwise(key_bytes, dtype, pooling):
-    rng = np.random.default_rng(900 + key_bytes + 10 * dtype + pooling)
-    rows, dim, bags, hot = 20000, 128, 48, 600
+def test_cached_copies_equal_the_linear_table_bitwise(shape, key_bytes, dtype, pooling):
+    rng = np.random.default_rng(900 + key_bytes + 10 * dtype + pooling + shape[1])
+    rows, dim = 20000, 128
+    bags, hot = shape
     tb = float_table(rng, rows, dim, dtype, dyadic_values=False)
     ct = CachedTable(tb, 1 << 20, key_bytes, value_dtype=DT[dtype])
     kt = np.int64 if key_bytes == 8 else np.int32
@@ -93,18 +96,19 @@ def test_cached_copies_equal_the_linear_table_bitwise(key_bytes, dtype, pooling)
     close(layer, lctx, ct)
 
 
-def test_hit_miss_decisions_against_the_cache_model():
+@pytest.mark.parametrize("lens", [(300, 1500), (1, 40)], ids=["long", "short"])
+def test_hit_miss_decisions_against_the_cache_model(lens):
     """Cached values negated: every key's source shows in the output.  CSR bags
-    of 300 to 1500 keys, one empty."""
-    rng = np.random.default_rng(918)
-    rows, dim, bags = 30000, 128, 40
+    of 300 to 1500 keys (or 1 to 40), one empty."""
+    rng = np.random.default_rng(918 + lens[0])
+    rows, dim, bags = 30000, 128, 40 if lens[0] > 1 else 600
     tb = float_table(rng, rows, dim, O.F32, dyadic_values=False)
     ct = CachedTable(tb, 2 << 20, 8)
     ct.model.insert_keys(rng.choice(8000, size=9000).astype(np.int64), uvm=ct.uvm_np.reshape(-1))
     d = ct.model.data()
     d.reshape(-1, 4)[:, 3] ^= np.uint8(0x80)
     ct.load_model()
-    lens = rng.integers(300, 1500, size=bags)
+    lens = rng.integers(lens[0], lens[1], size=bags)
     lens[5] = 0
     off = np.zeros(bags + 1, np.int64)
     off[1:] = np.cumsum(lens)
