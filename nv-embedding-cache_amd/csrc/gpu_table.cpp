@@ -303,6 +303,9 @@ void GpuTable::import_state(const void* tags, const float* counters, const int64
     if (counters) NVE_HIP(hipMemcpy(h_counters_.data(), counters, ways * sizeof(float), hipMemcpyDefault));
     if (set_ts) NVE_HIP(hipMemcpy(h_set_ts_.data(), set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
   }
+  // a copy from pageable memory may still be in flight when hipMemcpy returns;
+  // lookups on any stream after this call must see the imported state
+  NVE_HIP(hipDeviceSynchronize());
   global_ts_ = global_ts;
 }
 

@@ -110,6 +110,8 @@ def _hip_lib():
         h.hipHostFree.argtypes = [ctypes.c_void_p]
         h.hipMemcpy.restype = ctypes.c_int
         h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        h.hipDeviceSynchronize.restype = ctypes.c_int
+        h.hipDeviceSynchronize.argtypes = []
         _hip = h
     return _hip
 
@@ -151,6 +153,10 @@ class MemBlock:
         import numpy as np
         src_bytes = np.frombuffer(mv.cast("B"), dtype=np.uint8)
         rc = _hip_lib().hipMemcpy(self._ptr, src_bytes.ctypes.data, nbytes, 4)  # hipMemcpyDefault
+        if rc == 0:
+            # from pageable memory the copy may still be in flight when hipMemcpy
+            # returns; lookups on other streams must see the whole block
+            rc = _hip_lib().hipDeviceSynchronize()
         if rc != 0:
             raise _lib.NVEError(_lib.HIP_ERROR, f"copy_from: hipMemcpy failed ({rc})")
 

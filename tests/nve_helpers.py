@@ -151,3 +151,6 @@ def hip_memcpy(dst, src, nbytes):
         _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
     rc = _hip.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 4)
     assert rc == 0, f"hipMemcpy failed: {rc}"
+    # from pageable memory hipMemcpy may return once the source is staged, before
+    # the device has the bytes; kernels on other streams must not start earlier
+    assert _hip.hipDeviceSynchronize() == 0
