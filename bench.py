@@ -503,8 +503,10 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the lookup path is single-GPU; "
-              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the lookup path is single-GPU; across GPUs "
+              "it would shard the table by rows: local dedup, an all-to-all of unique keys to their "
+              "owners, find-and-pool there, an all-to-all of rows back). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
