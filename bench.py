@@ -128,6 +128,63 @@ def read_ceiling(torch, lib, stream, counts):
     return res
 
 
+def step_spread(torch, stream, step, groups=20, per_group=10):
+    """Spread of the step time: `groups` runs of `per_group` back-to-back steps,
+    each bracketed by events on `stream` (an event between every single step
+    would add its own cost to a step of a few microseconds); median, p10 and
+    p90 over the groups of the mean step time, in microseconds."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    evs[0].record(stream)
+    for g in range(groups):
+        for i in range(per_group):
+            step(g * per_group + i)
+        evs[g + 1].record(stream)
+    torch.cuda.synchronize()
+    t = sorted(evs[g].elapsed_time(evs[g + 1]) * 1e3 / per_group for g in range(groups))
+
+    def q(f):
+        return round(t[min(groups - 1, int(f * groups))], 3)
+
+    return {"groups": groups, "steps_per_group": per_group, "median_us": q(0.5), "p10_us": q(0.1),
+            "p90_us": q(0.9)}
+
+
+def f16_ulp(torch, x):
+    """Spacing of fp16 numbers at |x| (x float64): 2^(floor(log2|x|) - 10), at least 2^-24."""
+    _, e = torch.frexp(x)
+    return torch.clamp(torch.ldexp(torch.ones_like(x), (e - 11).to(torch.int32)), min=2.0 ** -24)
+
+
+def check_pooled_bags(torch, table, keys, out, hot, bag_ids):
+    """Untimed check of sampled bags of a Fixed-hotness Sum lookup against
+    torch's own gather summed in float64: each fp16 output within one fp16
+    ulp of the exact sum, or within 1e-5 of the row's largest magnitude."""
+    for b in bag_ids:
+        ref = table[keys[b * hot:(b + 1) * hot]].double().sum(0)
+        got = out[b].double()
+        tol = f16_ulp(torch, ref.half().double()) + 1e-5 * ref.abs().max()
+        bad = int(((got - ref).abs() > tol).sum().item())
+        if bad:
+            raise SystemExit(f"bench.py: pooled bag {b} differs from its float64 sum in {bad} elements")
+    return len(bag_ids)
+
+
+def zipf_ceiling(torch, lib, stream, table, row_bytes, batches, launches=100):
+    """Read ceiling on the workload's own keys: the random-row read kernel
+    fetching row key[i] of the workload's table for every key of a batch
+    (same rows, same L2/MALL reuse, no pooling), cycling the batches."""
+    sink = torch.zeros((batches[0].numel() + 127) // 128, dtype=torch.int32, device="cuda")
+    s = ctypes.c_void_p(stream.cuda_stream)
+    n = batches[0].numel()
+
+    def launch(i):
+        lib.call("nve_amd_read_ceiling", ctypes.c_void_p(table.data_ptr()), row_bytes,
+                 ctypes.c_void_p(batches[i % len(batches)].data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
+
+    ms = time_steps(torch, stream, launch, 5, launches)
+    return (n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms * 1e3
+
+
 def time_steps(torch, stream, step, warmup, steps):
     """Mean milliseconds per step between HIP events recorded on `stream`."""
     for i in range(warmup):
@@ -585,6 +642,13 @@ def main():
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     log(f"timed {args.steps} steps: {ms * 1000:.2f} us/step (events), wall {wall * 1e3 / args.steps * 1000:.2f} us/step")
+    # untimed: the spread of single steps, then the last batch's output checked on sampled bags
+    spread = step_spread(torch, stream, step)
+    step(0)
+    torch.cuda.synchronize()
+    checked = check_pooled_bags(torch, d_table, batches[0], out, hot,
+                                sorted({0, 1, bags // 2, bags - 1, 7 % bags, (bags * 3) // 4}))
+    log(f"step spread {spread}; {checked} sampled bags match their float64 sums")
 
     # algorithmic bytes per launch: keys + one stored row per key + pooled output
     alg = nkeys * 8 + nkeys * width + bags * width
@@ -596,6 +660,13 @@ def main():
     if os.path.exists(tf):
         with open(tf) as f:
             roof["traffic"] = json.load(f).get("traffic_bytes_per_launch")
+    if roof["traffic"]:
+        # DRAM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel and workload, committed
+        # profile) over this run's kernel time: the HBM fraction net of L2 / MALL reuse
+        dram = roof["traffic"] / (ms * 1e-3) / 1e9
+        roof["achieved_dram"] = round(dram, 1)
+        roof["frac_dram"] = round(dram / HBM_PEAK_GBPS, 4)
+        roof["traffic_source"] = "profiles/pool_split_kernel_c2pool_traffic.md (rocprofv3 --pmc)"
     result = {"metric": METRIC, "value": round(nkeys / (ms * 1e-3), 1), "unit": "lookups/s",
               "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -603,9 +674,15 @@ def main():
               "config": {"workload": "C2-pool: GPUEmbeddingLayer fused find-and-pool, fp16 table in HBM",
                          "table_rows": rows, "dim": dim, "row_dtype": "f16", "keys_per_batch": nkeys,
                          "zipf_alpha": args.alpha, "bags": bags, "hotness": hot, "pooling": "sum",
-                         "output_dtype": "f16", "accumulate": "f32", "key_batches_cycled": args.batches},
+                         "output_dtype": "f16", "accumulate": "f32", "key_batches_cycled": args.batches,
+                         "checked_bags": checked},
+              "step_spread": spread,
               "roofline": roof}
     if not args.no_ceiling:
+        zc, zus = zipf_ceiling(torch, _lib, stream, d_table, width, batches)
+        log(f"read ceiling on the workload's own keys and table: {zc:.0f} GB/s ({zus:.1f} us per batch)")
+        roof["zipf_read_ceiling_GBps"] = round(zc, 1)
+        roof["frac_of_zipf_ceiling"] = round(achieved / zc, 4)
         # same number of rows per launch as one batch, and 4x that (closer to asymptotic)
         c = read_ceiling(torch, _lib, stream, [nkeys, 4 * nkeys])
         (c1, us1), (c4, us4) = c[nkeys], c[4 * nkeys]
