@@ -117,6 +117,24 @@ NVE_C_API nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out);
 NVE_C_API nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx,
                                                      int64_t n, const void* keys);
 
+/* LinearHostTable (include/linear_host_table.hpp:36-183): a dense table of
+ * num_rows rows of config->max_value_size bytes at emb_table (host memory the
+ * caller owns and keeps alive), row k at emb_table + k * max_value_size,
+ * values of config->value_dtype (FLOAT32, FLOAT16 or a rowwise-quantized
+ * type); config->key_size must match key_type.  At most max_threads tasks run
+ * per operation (<= 0: no limit beyond the context's thread pool).  The
+ * reference builds this table inside its pynve HostEmbedding binding
+ * (python/pynve/bindings/binding_layers.hpp:742-756); its C ABI has no
+ * constructor for it.  The handle works with nve_table_find / update /
+ * update_accumulate (FLOAT32 rows) / insert / erase / clear (the last three
+ * have no effect), the getters (device id -1), the lookup counter (keys
+ * found) and nve_host_embedding_layer_create.  Nothing it does enters the HIP
+ * runtime while its buffers are host memory. */
+NVE_C_API nve_status_t nve_amd_linear_host_table_create(nve_table_t* out, nve_key_type_t key_type,
+                                                        const nve_host_table_config_t* config,
+                                                        void* emb_table, int64_t num_rows,
+                                                        int64_t max_threads);
+
 /* Training backprop: the sparse gradient of a lookup with respect to the table
  * (GradientCalculator::compute_gradients, cuda_ops/gradient_calculator.cuh:238-301,
  * which the reference's pynve GPU bindings call as concat_backprop /

@@ -11,6 +11,7 @@
 #include "../../include/nve_amd_ext.h"
 #include "backprop.hpp"
 #include "dedup.hpp"
+#include "host_layer.hpp"
 #include "layers.hpp"
 
 using namespace nve_amd;
@@ -18,8 +19,10 @@ using namespace nve_amd;
 struct nve_context_s {
   std::shared_ptr<ExecutionContext> ptr;
 };
+// A table handle holds a GPU table (8-way cache) or a linear host table.
 struct nve_table_s {
   std::shared_ptr<GpuTable> ptr;
+  std::shared_ptr<LinearHostTable> host;
 };
 struct nve_layer_s {
   std::shared_ptr<EmbeddingLayer> ptr;
@@ -318,7 +321,7 @@ nve_status_t nve_table_destroy(nve_table_t table) {
 }
 
 #define NEED_TABLE_CTX                                                       \
-  if (!table || !table->ptr || !ctx || !ctx->ptr)                            \
+  if (!table || (!table->ptr && !table->host) || !ctx || !ctx->ptr)          \
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and ctx must not be NULL");
 
 nve_status_t nve_table_find(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys,
@@ -326,7 +329,10 @@ nve_status_t nve_table_find(nve_table_t table, nve_context_t ctx, int64_t n, con
                             int64_t* value_sizes) {
   NEED_TABLE_CTX
   C_TRY
-  table->ptr->find(*ctx->ptr, n, keys, hit_mask, value_stride, values, value_sizes);
+  if (table->host)
+    table->host->find_any(*ctx->ptr, n, keys, hit_mask, value_stride, values, value_sizes);
+  else
+    table->ptr->find(*ctx->ptr, n, keys, hit_mask, value_stride, values, value_sizes);
   return NVE_SUCCESS;
   C_CATCH
 }
@@ -335,6 +341,7 @@ nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, c
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
   C_TRY
+  if (table->host) return NVE_SUCCESS;  // a linear host table holds every row: no effect
   table->ptr->insert(*ctx->ptr, n, keys, value_stride, value_size, values);
   return NVE_SUCCESS;
   C_CATCH
@@ -344,7 +351,10 @@ nve_status_t nve_table_update(nve_table_t table, nve_context_t ctx, int64_t n, c
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
   C_TRY
-  table->ptr->update(*ctx->ptr, n, keys, value_stride, value_size, values);
+  if (table->host)
+    table->host->update(*ctx->ptr, n, keys, value_stride, value_size, values);
+  else
+    table->ptr->update(*ctx->ptr, n, keys, value_stride, value_size, values);
   return NVE_SUCCESS;
   C_CATCH
 }
@@ -355,8 +365,12 @@ nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, i
                                          nve_data_type_t value_type) {
   NEED_TABLE_CTX
   C_TRY
-  table->ptr->update_accumulate(*ctx->ptr, n, keys, value_stride, value_size, values,
-                                dtype_in(value_type));
+  if (table->host)
+    table->host->update_accumulate(*ctx->ptr, n, keys, value_stride, value_size, values,
+                                   dtype_in(value_type));
+  else
+    table->ptr->update_accumulate(*ctx->ptr, n, keys, value_stride, value_size, values,
+                                  dtype_in(value_type));
   return NVE_SUCCESS;
   C_CATCH
 }
@@ -364,6 +378,7 @@ nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, i
 nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
   NEED_TABLE_CTX
   C_TRY
+  if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
   table->ptr->clear(*ctx->ptr);
   return NVE_SUCCESS;
   C_CATCH
@@ -372,6 +387,7 @@ nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
 nve_status_t nve_table_erase(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys) {
   NEED_TABLE_CTX
   C_TRY
+  if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
   table->ptr->erase(*ctx->ptr, n, keys);
   return NVE_SUCCESS;
   C_CATCH
@@ -381,10 +397,15 @@ nve_status_t nve_table_create_execution_context(nve_table_t table, nve_context_t
                                                 void* lookup_stream, void* modify_stream,
                                                 nve_thread_pool_t thread_pool,
                                                 nve_allocator_t allocator) {
-  if (!table || !table->ptr || !out)
+  if (!table || (!table->ptr && !table->host) || !out)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");
   C_TRY
   NVE_CHECK_ARG(allocator == nullptr, "Custom allocators are not supported by this build");
+  if (table->host) {
+    *out = new nve_context_s{table->host->create_execution_context(
+        (hipStream_t)lookup_stream, (hipStream_t)modify_stream, unwrap(thread_pool))};
+    return NVE_SUCCESS;
+  }
   *out = new nve_context_s{std::make_shared<ExecutionContext>(
       table->ptr->config().device_id, (hipStream_t)lookup_stream, (hipStream_t)modify_stream,
       unwrap(thread_pool))};
@@ -393,29 +414,33 @@ nve_status_t nve_table_create_execution_context(nve_table_t table, nve_context_t
 }
 
 nve_status_t nve_table_get_device_id(const nve_table_t table, int32_t* out) {
-  if (!table || !table->ptr || !out)
+  if (!table || (!table->ptr && !table->host) || !out)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");
-  *out = table->ptr->config().device_id;
+  *out = table->host ? -1 : table->ptr->config().device_id;
   return NVE_SUCCESS;
 }
 
 nve_status_t nve_table_get_max_row_size(const nve_table_t table, int64_t* out) {
-  if (!table || !table->ptr || !out)
+  if (!table || (!table->ptr && !table->host) || !out)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");
-  *out = table->ptr->config().row_size_in_bytes;
+  *out = table->host ? table->host->config().row_bytes : table->ptr->config().row_size_in_bytes;
   return NVE_SUCCESS;
 }
 
 nve_status_t nve_table_get_key_size(const nve_table_t table, int64_t* out) {
-  if (!table || !table->ptr || !out)
+  if (!table || (!table->ptr && !table->host) || !out)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");
-  *out = table->ptr->key_bytes();
+  *out = table->host ? table->host->key_bytes() : table->ptr->key_bytes();
   return NVE_SUCCESS;
 }
 
 nve_status_t nve_table_reset_lookup_counter(nve_table_t table, nve_context_t ctx) {
   NEED_TABLE_CTX
   C_TRY
+  if (table->host) {
+    ctx->ptr->host_lookup_counter() = 0;
+    return NVE_SUCCESS;
+  }
   if (table->ptr->config().count_misses) {
     ScopedDevice sd(table->ptr->config().device_id);
     ctx->ptr->reset_misses();
@@ -429,6 +454,10 @@ nve_status_t nve_table_get_lookup_counter(const nve_table_t table, nve_context_t
   NEED_TABLE_CTX
   if (!counter) return set_error(NVE_ERROR_INVALID_ARGUMENT, "counter must not be NULL");
   C_TRY
+  if (table->host) {  // a host table counts the keys it resolved (host_table.hpp:363)
+    *counter = ctx->ptr->host_lookup_counter();
+    return NVE_SUCCESS;
+  }
   if (!table->ptr->config().count_misses) {
     *counter = 0;
   } else {
@@ -478,7 +507,7 @@ nve_status_t nve_linear_uvm_layer_create(nve_layer_t* out, nve_key_type_t key_ty
                                          const nve_linear_uvm_layer_config_t* config,
                                          nve_table_t gpu_table, nve_allocator_t allocator) {
   if (!out || !config || !gpu_table || !gpu_table->ptr)
-    return set_error(NVE_ERROR_INVALID_ARGUMENT, "out, config and gpu_table must not be NULL");
+    return set_error(NVE_ERROR_INVALID_ARGUMENT, "out, config and gpu_table must not be NULL (a GPU table)");
   C_TRY
   NVE_CHECK_ARG(allocator == nullptr, "Custom allocators are not supported by this build");
   LinearUVMLayerConfig c;
@@ -501,13 +530,28 @@ nve_status_t nve_hierarchical_layer_create(nve_layer_t* out, nve_key_type_t,
                    "Hierarchical (host / remote tier) layers are not part of this build");
 }
 
-nve_status_t nve_host_embedding_layer_create(nve_layer_t* out, nve_key_type_t,
-                                             const nve_host_embedding_layer_config_t*,
-                                             nve_table_t host_table, nve_allocator_t) {
-  if (out) *out = nullptr;
-  if (!host_table) return set_error(NVE_ERROR_INVALID_ARGUMENT, "host_table must not be NULL");
-  // host tables come only from plugin factories, which this build does not ship
-  return set_error(NVE_ERROR_INVALID_ARGUMENT, "host_table must be a host table");
+nve_status_t nve_host_embedding_layer_create(nve_layer_t* out, nve_key_type_t key_type,
+                                             const nve_host_embedding_layer_config_t* config,
+                                             nve_table_t host_table, nve_allocator_t allocator) {
+  if (!out || !config || !host_table)
+    return set_error(NVE_ERROR_INVALID_ARGUMENT, "out, config and host_table must not be NULL");
+  *out = nullptr;
+  // host tables come from nve_amd_linear_host_table_create (the plugin
+  // factories that produce other host tables are not part of this build)
+  if (!host_table->host)
+    return set_error(NVE_ERROR_INVALID_ARGUMENT, "host_table must be a host table (device id < 0)");
+  C_TRY
+  NVE_CHECK_ARG(allocator == nullptr, "Custom allocators are not supported by this build");
+  HostEmbeddingLayerConfig c;
+  c.layer_name = config->layer_name ? config->layer_name : "";
+  if (config->default_embedding_size > 0) {
+    NVE_CHECK_ARG(config->default_embedding != nullptr, "default_embedding must not be NULL");
+    const uint8_t* d = static_cast<const uint8_t*>(config->default_embedding);
+    c.default_embedding.assign(d, d + config->default_embedding_size);
+  }
+  *out = new nve_layer_s{std::make_shared<HostEmbeddingLayer>(key_bytes_of(key_type), c, host_table->host)};
+  return NVE_SUCCESS;
+  C_CATCH
 }
 
 nve_status_t nve_layer_destroy(nve_layer_t layer) {
@@ -922,6 +966,7 @@ nve_status_t nve_amd_gpu_table_import_state(nve_table_t table, const void* tags,
 nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx, int64_t n,
                                            const void* keys) {
   NEED_TABLE_CTX
+  if (!table->ptr) return set_error(NVE_ERROR_INVALID_ARGUMENT, "table must be a GPU table");
   C_TRY
   table->ptr->insert_from_uvm(*ctx->ptr, n, keys);
   return NVE_SUCCESS;
@@ -933,6 +978,26 @@ nve_status_t nve_amd_gpu_table_data(nve_table_t table, void** out) {
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and out must not be NULL");
   *out = table->ptr->data_ptr();
   return NVE_SUCCESS;
+}
+
+nve_status_t nve_amd_linear_host_table_create(nve_table_t* out, nve_key_type_t key_type,
+                                              const nve_host_table_config_t* config, void* emb_table,
+                                              int64_t num_rows, int64_t max_threads) {
+  if (!out || !config) return set_error(NVE_ERROR_INVALID_ARGUMENT, "out and config must not be NULL");
+  C_TRY
+  const int kb = key_bytes_of(key_type);
+  NVE_CHECK_ARG(config->key_size == kb, "config->key_size (", config->key_size,
+                ") differs from the key type's size (", kb, ")");
+  LinearHostTableConfig c;
+  c.emb_table = emb_table;
+  c.num_rows = num_rows;
+  c.row_bytes = config->max_value_size;
+  c.value_dtype = dtype_in(config->value_dtype);
+  c.max_threads = max_threads > 0 ? max_threads : INT64_MAX;
+  c.invalid_key = config->invalid_key;
+  *out = new nve_table_s{nullptr, std::make_shared<LinearHostTable>(kb, c)};
+  return NVE_SUCCESS;
+  C_CATCH
 }
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 
 #include "kernels/cache_launch.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -153,8 +154,12 @@ ExecutionContext::~ExecutionContext() {
     wait();
   } catch (...) {
   }
+  for (auto& kv : bufs_)
+    if (kv.second.plain) std::free(kv.second.ptr);
+  if (device_ < 0 && misses_ == nullptr) return;  // a host context holds no HIP memory
   ScopedDevice sd(device_);
   for (auto& kv : bufs_) {
+    if (kv.second.plain) continue;
     if (kv.second.host)
       (void)hipHostFree(kv.second.ptr);
     else
@@ -163,9 +168,29 @@ ExecutionContext::~ExecutionContext() {
   if (misses_) (void)hipFree(misses_);
 }
 
+void* ExecutionContext::host_buffer(const std::string& name, size_t bytes) {
+  std::lock_guard<std::mutex> lk(bufs_mu_);
+  Buf& b = bufs_[name];
+  NVE_CHECK(b.ptr == nullptr || b.plain, "Context buffer '", name, "' is not a host buffer");
+  if (b.ptr && b.bytes < bytes) {
+    std::free(b.ptr);
+    b.ptr = nullptr;
+  }
+  if (!b.ptr) {
+    const size_t sz = (std::max<size_t>(bytes, 256) + 63) / 64 * 64;
+    b.ptr = std::aligned_alloc(64, sz);
+    if (!b.ptr) throw Error(NVE_ERROR_OUT_OF_MEMORY, cat("Out of host memory for ", sz, " bytes"));
+    b.bytes = sz;
+    b.host = true;
+    b.plain = true;
+  }
+  return b.ptr;
+}
+
 void* ExecutionContext::buffer(const std::string& name, size_t bytes, bool host) {
   std::lock_guard<std::mutex> lk(bufs_mu_);
   Buf& b = bufs_[name];
+  NVE_CHECK(!b.plain, "Context buffer '", name, "' is a plain host buffer");
   if (b.ptr && (b.bytes < bytes || b.host != host)) {
     // the stream may still use the old buffer
     NVE_HIP(hipStreamSynchronize(lookup_));
@@ -232,9 +257,11 @@ void ExecutionContext::wait() {
       if (!first) first = std::current_exception();
     }
   }
-  ScopedDevice sd(device_);
-  NVE_HIP(hipStreamSynchronize(lookup_));
-  NVE_HIP(hipStreamSynchronize(modify_));
+  if (device_ >= 0) {  // a host context runs everything on the calling threads
+    ScopedDevice sd(device_);
+    NVE_HIP(hipStreamSynchronize(lookup_));
+    NVE_HIP(hipStreamSynchronize(modify_));
+  }
   if (first) std::rethrow_exception(first);
 }
 

@@ -136,6 +136,12 @@ class ExecutionContext {
   // Device (host = false) or pinned host (host = true) buffer of at least
   // `bytes`, kept under `name` and reused by later calls on this context.
   void* buffer(const std::string& name, size_t bytes, bool host = false);
+  // Ordinary (pageable, 64-byte aligned) host memory under `name`: what a
+  // context of the host layer uses, so that it never enters the HIP runtime.
+  void* host_buffer(const std::string& name, size_t bytes);
+
+  // Lookup counter of a host table (LinearHostTable counts resolved keys).
+  int64_t& host_lookup_counter() { return host_counter_; }
 
   // Device counter of cache misses (zeroed by reset_misses on lookup_stream).
   unsigned long long* miss_counter();
@@ -150,6 +156,7 @@ class ExecutionContext {
     void* ptr = nullptr;
     size_t bytes = 0;
     bool host = false;
+    bool plain = false;  // host_buffer: malloc'd, not pinned
   };
   int device_;
   hipStream_t lookup_, modify_;
@@ -157,6 +164,7 @@ class ExecutionContext {
   std::mutex bufs_mu_;  // the lookup thread and a pool task (auto-insert) share buffers
   std::map<std::string, Buf> bufs_;
   unsigned long long* misses_ = nullptr;
+  int64_t host_counter_ = 0;
   std::mutex pending_mu_;
   std::vector<std::future<void>> pending_;
 };

@@ -152,6 +152,7 @@ SIGNATURES = {
     "nve_amd_gpu_table_import_state": (I32, [P, P, P, P, I64]),
     "nve_amd_gpu_table_data": (I32, [P, PP]),
     "nve_amd_table_insert_from_uvm": (I32, [P, P, I64, P]),
+    "nve_amd_linear_host_table_create": (I32, [PP, ctypes.c_int, ctypes.POINTER(HostTableConfig), P, I64, I64]),
     "nve_amd_backprop_workspace_size": (I32, [I64, I64, I64, ctypes.POINTER(U64)]),
     "nve_amd_pooling_backprop": (I32, [ctypes.c_int, I64, P, ctypes.c_int, ctypes.c_int, P, I64, I64, P, I32,
                                        P, I32, I64, P, P, PI64, P, U64, P]),

@@ -18,8 +18,9 @@ page faults, which is what the reference's advice arranges.
 Table checkpoints (`TensorFileFormat`, `write_tensor_to_stream`,
 `load_tensor_from_stream`) read and write the reference's .nve container.
 
-Out of this build (raise NotImplementedInBuild): HostEmbedding / HierarchicalEmbedding layers, the parameter-server tables and
-the multi-process memory blocks (NVL / MPI / Dist*).
+Out of this build (raise NotImplementedInBuild): the HierarchicalEmbedding
+layer, the parameter-server tables and the multi-process memory blocks
+(NVL / MPI / Dist*).
 """
 import ctypes
 import json
@@ -182,6 +183,16 @@ class _PinnedHost(MemBlock):
         if getattr(self, "_ptr", 0) and _hip is not None:
             _hip.hipHostFree(self._ptr)
             self._ptr = 0
+
+
+class _PlainHost(MemBlock):
+    """Ordinary (pageable) host memory, for a host layer on a machine without a
+    GPU driver: the rows live in a numpy buffer this block owns."""
+
+    def __init__(self, kind, size):
+        import numpy as np
+        self._buf = np.zeros(max(int(size), 1), dtype=np.uint8)
+        super().__init__(kind, self._buf.ctypes.data, size)
 
 
 class HostMemBlock(_PinnedHost):
@@ -520,8 +531,52 @@ class LinearUVMEmbedding(NVEmbedBinding):
 
 
 class HostEmbedding(NVEmbedBinding):
-    def __init__(self, *args, **kwargs):
-        _not_in_build("HostEmbedding (the CPU host layer)")
+    """Host-only layer (binding_layers.hpp:730-789): a LinearHostTable over the
+    memory block's rows and the host embedding layer on top of it.  Lookups,
+    pooling and updates run on CPU threads inside libnve_amd.so; with host
+    buffers (device_id < 0) nothing touches a GPU.  Inference only: the
+    backprop entries raise."""
+
+    def __init__(self, row_size, num_embeddings, dtype, mem_block, device_id=-1, config=None):
+        config = config if config is not None else EmbedLayerConfig()
+        super().__init__(device_id, row_size, dtype, config)
+        self.num_embeddings_ = int(num_embeddings)
+        self.row_size_ = int(row_size)
+        self.mem_block_ = mem_block
+        self._table = None
+        L = _lib.load()
+        tcfg = L.nve_host_table_config_default()
+        tcfg.key_size = 8
+        tcfg.max_value_size = self.row_size_in_bytes_
+        tcfg.value_dtype = int(self.data_type_)
+        t = ctypes.c_void_p()
+        _lib.call("nve_amd_linear_host_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(tcfg),
+                  ctypes.c_void_p(mem_block.get_ptr()), self.num_embeddings_, 0)
+        self._table = t.value
+        try:
+            lcfg = L.nve_host_embedding_layer_config_default()
+            lcfg.layer_name = b"host_layer"
+            default = bytes(bytearray(config.default_embedding))
+            self._default_row = ctypes.create_string_buffer(default, len(default) or 1)
+            if default:
+                lcfg.default_embedding = ctypes.cast(self._default_row, ctypes.c_void_p)
+                lcfg.default_embedding_size = len(default)
+            h = ctypes.c_void_p()
+            _lib.call("nve_host_embedding_layer_create", ctypes.byref(h), _lib.KEY_INT64, ctypes.byref(lcfg),
+                      self._table, None)
+            self._layer = h.value
+        except Exception:
+            _lib._lib.nve_table_destroy(self._table)
+            self._table = None
+            raise
+
+    def _destroy(self):
+        try:
+            super()._destroy()
+        finally:
+            if getattr(self, "_table", None) is not None and _lib._lib is not None:
+                _lib._lib.nve_table_destroy(self._table)
+                self._table = None
 
 
 class HierarchicalEmbedding(NVEmbedBinding):
@@ -697,11 +752,11 @@ def _table_geometry(layer):
     if isinstance(layer, LinearUVMEmbedding):
         esize = 4 if layer.data_type_ == DataType_t.Float32 else 2
         return layer.num_embeddings_, layer.row_size_, esize, layer.mem_block_.get_ptr()
-    if isinstance(layer, GPUEmbedding):
+    if isinstance(layer, (GPUEmbedding, HostEmbedding)):
         return (layer.num_embeddings_, layer.row_size_, dtype_size(layer.data_type_),
                 layer.mem_block_.get_ptr())
-    raise TypeError("write_tensor_to_stream / load_tensor_from_stream take a LinearUVMEmbedding "
-                    f"or a GPUEmbedding, not {type(layer).__name__}")
+    raise TypeError("write_tensor_to_stream / load_tensor_from_stream take a LinearUVMEmbedding, "
+                    f"a GPUEmbedding or a HostEmbedding, not {type(layer).__name__}")
 
 
 def _device_chunks(layer, base, nbytes):
@@ -728,7 +783,7 @@ def write_tensor_to_stream(layer, stream, name):
     rows, cols, esize, base = _table_geometry(layer)
     nbytes = rows * cols * esize
     fmt = TensorFileFormat()
-    if isinstance(layer, LinearUVMEmbedding):
+    if isinstance(layer, (LinearUVMEmbedding, HostEmbedding)):  # host memory, written in place
         fmt.write_tensor_to_stream(stream, name, rows, cols, esize, [_host_view(base, nbytes)])
     else:
         fmt.write_tensor_to_stream(stream, name, rows, cols, esize, _device_chunks(layer, base, nbytes))
@@ -747,7 +802,7 @@ def load_tensor_from_stream(layer, stream, name):
     nbytes = rows * cols * esize
     s = _PyStream(stream)
     found = TensorFileFormat().find_tensor(s, name, rows, cols, esize)
-    if isinstance(layer, LinearUVMEmbedding):
+    if isinstance(layer, (LinearUVMEmbedding, HostEmbedding)):
         if found is not None and s.read_into(_host_view(base, nbytes)) != nbytes:
             raise _lib.NVEError(_lib.RUNTIME, "Problem reading tensor")
         return

@@ -2,7 +2,7 @@
 
 The two ops of the reference's torch library (torch_binding.cpp:85-92) are
 defined here with the same schemas and implemented for HIP tensors (torch's
-"CUDA" dispatch key on ROCm):
+"CUDA" dispatch key on ROCm) and for host tensors ("CPU": host layers):
 
     nve_ops::embedding_lookup(Tensor marker, Tensor keys, int embedding_size,
                               int dtype) -> Tensor
@@ -18,7 +18,6 @@ pynve/torch/__init__.py does.
 import torch
 
 from .. import nve
-from .. import _lib
 
 HAS_TORCH_OPS = True
 
@@ -57,23 +56,28 @@ def _check_pooling_weights(w, num_keys):
     raise RuntimeError("nve-torch-ops: weights must be a float32 or float16 tensor")
 
 
-def _embedding_lookup_hip(marker, keys, embedding_size, dtype):
-    """nve_torch_ops.cu:67-98: [num_keys, dim] rows of the layer's dtype,
-    looked up on the keys' device's current stream."""
+def _stream_for(t):
+    """The stream a lookup on tensor t's device runs on (0 for host tensors:
+    a host layer runs on the calling threads)."""
+    return torch.cuda.current_stream(t.device).cuda_stream if t.is_cuda else 0
+
+
+def _embedding_lookup_impl(marker, keys, embedding_size, dtype):
+    """nve_torch_ops.cu:67-98 / nve_torch_ops_cpu.cpp:59-90: [num_keys, dim]
+    rows of the layer's dtype, on the keys' device."""
     _check_index_tensor(keys, "keys")
     binding = nve.get_binding(marker.data_ptr())
     n = keys.numel()
     out = torch.empty((n, binding.get_embedding_dim()), dtype=_out_dtype(int(binding.get_data_type())),
                       device=keys.device)
-    stream = torch.cuda.current_stream(keys.device).cuda_stream
-    binding.lookup(n, keys.data_ptr(), out.data_ptr(), stream)
+    binding.lookup(n, keys.data_ptr(), out.data_ptr(), _stream_for(keys))
     return out
 
 
-def _embedding_lookup_with_pooling_hip(marker, keys, offsets, weights, pooling_type,
-                                       embedding_size, dtype):
-    """nve_torch_ops.cu:100-146: [num_bags, dim] pooled rows, CSR offsets
-    with num_bags + 1 entries."""
+def _embedding_lookup_with_pooling_impl(marker, keys, offsets, weights, pooling_type,
+                                        embedding_size, dtype):
+    """nve_torch_ops.cu:100-146 / nve_torch_ops_cpu.cpp:92-133: [num_bags, dim]
+    pooled rows, CSR offsets with num_bags + 1 entries."""
     _check_index_tensor(keys, "keys")
     _check_index_tensor(offsets, "offsets")
     if offsets.numel() < 2:
@@ -87,21 +91,17 @@ def _embedding_lookup_with_pooling_hip(marker, keys, offsets, weights, pooling_t
     if weights is not None:
         wdt = _check_pooling_weights(weights, keys.numel())
         wptr = weights.data_ptr()
-    stream = torch.cuda.current_stream(keys.device).cuda_stream
     binding.lookup_with_pooling(keys.numel(), keys.data_ptr(), out.data_ptr(), int(pooling_type),
-                                offsets.numel(), offsets.data_ptr(), wdt, wptr, stream)
+                                offsets.numel(), offsets.data_ptr(), wdt, wptr, _stream_for(keys))
     return out
 
 
-def _host_layer_missing(*args, **kwargs):
-    raise _lib.NotImplementedInBuild(
-        _lib.NOT_IMPLEMENTED, "nve_ops on CPU tensors (the host layer) are not part of this build")
-
-
-_DEF.impl("embedding_lookup", _embedding_lookup_hip, "CUDA")
-_DEF.impl("embedding_lookup_with_pooling", _embedding_lookup_with_pooling_hip, "CUDA")
-_DEF.impl("embedding_lookup", _host_layer_missing, "CPU")
-_DEF.impl("embedding_lookup_with_pooling", _host_layer_missing, "CPU")
+# one implementation for both dispatch keys: the binding of the marker decides
+# where the lookup runs (HIP kernels, or CPU threads for a host layer), and
+# buffers on the other side are staged by the layer
+for _key in ("CUDA", "CPU"):
+    _DEF.impl("embedding_lookup", _embedding_lookup_impl, _key)
+    _DEF.impl("embedding_lookup_with_pooling", _embedding_lookup_with_pooling_impl, _key)
 
 
 @torch.library.register_fake("nve_ops::embedding_lookup")

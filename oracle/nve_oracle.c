@@ -335,6 +335,38 @@ void orc_pool(const uint8_t* const* rows, int dtype, int64_t count, int sparse, 
   free(acc);
 }
 
+/* One element as the CPU HostLayer widens it to float (cpu_pooling.hpp:68-150
+ * float/half, :166-259 and :302-341 quantized): float(x); quantized
+ * float(q)*scale + offset taken as one fma (offset 0 for the int8 formats, f16
+ * metadata widened first); the extension formats as dequant_elem. */
+static float host_value(const uint8_t* row, int dtype, int64_t count, int64_t i) {
+  switch (dtype) {
+    case ORC_F32: return ld_f32(row + 4 * i);
+    case ORC_F16: return orc_f16_to_f32(ld_u16(row + 2 * i));
+    case ORC_QI8_F32: return fmaf((float)(int8_t)row[i], ld_f32(row + count), 0.0f);
+    case ORC_QI8_F16: return fmaf((float)(int8_t)row[i], orc_f16_to_f32(ld_u16(row + count)), 0.0f);
+    case ORC_QU8_F32: return fmaf((float)row[i], ld_f32(row + count), ld_f32(row + count + 4));
+    case ORC_QU8_F16:
+      return fmaf((float)row[i], orc_f16_to_f32(ld_u16(row + count)),
+                  orc_f16_to_f32(ld_u16(row + count + 2)));
+    default: return elem_as_f32(dequant_elem(row, dtype, count, i));
+  }
+}
+
+/* cpu_kernel_concatenate / cpu_kernel_concatenate_quant (cpu_pooling.hpp:272-341):
+ * one output row per input row, out = cast(host_value), rounded to nearest even
+ * for an f16 output (no half rounding in between, unlike the GPU's f16-metadata
+ * dequantize). */
+void orc_convert_host(const uint8_t* row, int dtype, int64_t count, int out_dtype, void* out) {
+  for (int64_t i = 0; i < count; i++) {
+    const float v = host_value(row, dtype, count, i);
+    if (out_dtype == ORC_F16)
+      ((uint16_t*)out)[i] = orc_f32_to_f16(v);
+    else
+      ((float*)out)[i] = v;
+  }
+}
+
 /* cpu_pooling.hpp:68-150 (float/half) and :166-259 (quantized): per bag,
  * v = float(x) [quantized: float(q)*scale + offset, taken as one fma];
  * weighted: v *= w; acc += v; Mean: acc * (1/denom); zero denom -> zero row. */
@@ -361,21 +393,7 @@ void orc_pool_host(const uint8_t* const* rows, int dtype, int64_t count, int spa
       wsum += w;
       const uint8_t* row = rows[k];
       for (int64_t i = 0; i < count; i++) {
-        float v;
-        switch (dtype) {
-          case ORC_F32: v = ld_f32(row + 4 * i); break;
-          case ORC_F16: v = orc_f16_to_f32(ld_u16(row + 2 * i)); break;
-          case ORC_QI8_F32: v = fmaf((float)(int8_t)row[i], ld_f32(row + count), 0.0f); break;
-          case ORC_QI8_F16:
-            v = fmaf((float)(int8_t)row[i], orc_f16_to_f32(ld_u16(row + count)), 0.0f);
-            break;
-          case ORC_QU8_F32: v = fmaf((float)row[i], ld_f32(row + count), ld_f32(row + count + 4)); break;
-          case ORC_QU8_F16:
-            v = fmaf((float)row[i], orc_f16_to_f32(ld_u16(row + count)),
-                     orc_f16_to_f32(ld_u16(row + count + 2)));
-            break;
-          default: v = elem_as_f32(dequant_elem(row, dtype, count, i)); break;
-        }
+        float v = host_value(row, dtype, count, i);
         if (weighted) v *= w;
         acc[i] += v;
       }

@@ -20,7 +20,12 @@
  *   orc_dequant_row                      closed form float(q)*s(+o), numpy
  *   orc_pool (GPU order)                 dyadic-fraction table => exact Sum;
  *                                        torch.nn.EmbeddingBag in float64
- *   orc_pool_host (CPU HostLayer order)  torch.nn.EmbeddingBag, 1e-6
+ *   orc_pool_host (CPU HostLayer order)  torch.nn.EmbeddingBag, 1e-6; dyadic
+ *                                        tables exact; the element values of
+ *                                        every format by numpy closed forms
+ *   orc_convert_host                     numpy casts (f32 <-> f16) and the
+ *                                        float64 closed form of q*s+o, exact
+ *                                        in float64, rounded once
  *   orc_cache_*                          closed-form set/tag math, brute force
  *                                        residency invariants, hand-built cases
  *   orc_histogram                        brute force (collections.Counter)
@@ -108,6 +113,10 @@ void orc_pool_host(const uint8_t* const* rows, int dtype, int64_t count, int spa
                    int64_t num_keys, const void* offsets, int key_bytes, int64_t num_bags,
                    int64_t hotness, const void* weights, int weight_dtype, int out_dtype,
                    void* out, int64_t out_stride);
+
+/* CPU HostLayer Concatenate to another type: cpu_pooling.hpp:272-341, one row
+ * (count values of dtype) converted / dequantized to out_dtype. */
+void orc_convert_host(const uint8_t* row, int dtype, int64_t count, int out_dtype, void* out);
 
 /* Resolve linear-table row pointers (table + key*row_bytes). */
 void orc_linear_rows(const void* keys, int key_bytes, int64_t n, const uint8_t* table,

@@ -71,6 +71,7 @@ def _declare(L):
     L.orc_dequant_row.argtypes = [P, I32, I64, I32, P]
     L.orc_pool.argtypes = [P, I32, I64, I32, I32, I64, P, I32, I64, I64, P, I32, I32, P, I64]
     L.orc_pool_host.argtypes = L.orc_pool.argtypes
+    L.orc_convert_host.argtypes = [P, I32, I64, I32, P]
     L.orc_linear_rows.argtypes = [P, I32, I64, P, I64, P]
     L.orc_host_layer_lookup.argtypes = [P, I32, I64, P, U64, I64, I32, I32, I32, P, I64, I64, P,
                                         I32, I32, P, P, I64, I32]
@@ -179,6 +180,17 @@ def dequant_rows(rows_bytes, dtype, count, out_dtype):
     L = lib()
     for i in range(n):
         L.orc_dequant_row(_p(rows_bytes[i]), dtype, count, out_dtype, _p(out[i]))
+    return out
+
+
+def convert_rows_host(rows_bytes, dtype, count, out_dtype):
+    """CPU HostLayer Concatenate to out_dtype of (n, row_bytes) stored rows."""
+    rows_bytes = np.ascontiguousarray(rows_bytes, dtype=np.uint8)
+    n = rows_bytes.shape[0]
+    out = np.empty((n, count), out_np_dtype(out_dtype))
+    L = lib()
+    for i in range(n):
+        L.orc_convert_host(_p(rows_bytes[i]), dtype, count, out_dtype, _p(out[i]))
     return out
 
 
