@@ -12,9 +12,10 @@ Reported beside the throughput:
   roofline      algorithmic bytes per launch / the kernel's mean duration
                 (HIP events on the lookup stream) against the 8 TB/s HBM peak,
                 and against the measured random-row read ceiling;
-  cpu_baseline  the reference HostLayer algorithm (threaded gather + fp32
-                pooling, oracle/ restatement) timed on this host's cores on a
-                bounded sample of the same batches.
+  cpu_baseline  the product's CPU HostLayer (threaded gather + fp32 pooling,
+                restating the reference's) timed on this host's cores on
+                whole batches of the same workload, median with p10 / p90,
+                at the reference's default worker count and at all cores.
 """
 import argparse
 import ctypes
@@ -66,31 +67,89 @@ def cpu_info():
     return model, avail
 
 
-def cpu_baseline(torch, d_table, key_batches, bags, hot, rows, dim, seconds):
-    """HostLayer restatement (oracle/, the checker library) timed on host cores."""
-    import numpy as np
-    from oracle import oracle as O
+class HostLayerBaseline:
+    """The product's CPU HostLayer (LinearHostTable + HostEmbeddingLayer of
+    libnve_amd.so, a restatement of the reference's host_embedding_layer.cpp:
+    55-247 -> cpu_gather.hpp:28-80 -> cpu_pooling.hpp:68-150) over a host copy
+    of a table, on `threads` worker threads of its own pool."""
 
+    def __init__(self, lib, h_table, rows, row_bytes, dtype, threads):
+        L = lib.load()
+        self.lib, self.h_table = lib, h_table
+        self.pool, self.t, self.layer, self.ctx = (ctypes.c_void_p() for _ in range(4))
+        lib.call("nve_thread_pool_create", ctypes.byref(self.pool), f'{{"num_workers": {threads}}}'.encode())
+        tc = L.nve_host_table_config_default()
+        tc.key_size, tc.max_value_size, tc.value_dtype = 8, row_bytes, dtype
+        lib.call("nve_amd_linear_host_table_create", ctypes.byref(self.t), lib.KEY_INT64, ctypes.byref(tc),
+                 ctypes.c_void_p(h_table.ctypes.data), rows, 0)
+        lc = L.nve_host_embedding_layer_config_default()
+        lib.call("nve_host_embedding_layer_create", ctypes.byref(self.layer), lib.KEY_INT64, ctypes.byref(lc),
+                 self.t, None)
+        lib.call("nve_layer_create_execution_context", self.layer, ctypes.byref(self.ctx), None, None,
+                 self.pool, None)
+
+    def pooled(self, keys, out, out_stride, hot, out_dtype):
+        self.lib.check(self.lib.load().nve_layer_lookup_pooled(
+            self.layer, self.ctx, keys.size, ctypes.c_void_p(keys.ctypes.data), ctypes.c_void_p(out.ctypes.data),
+            out_stride, None, self.lib.POOL_SUM, self.lib.SPARSE_FIXED, None, 0, hot, None, 0, out_dtype, None))
+
+    def gather(self, keys, out, out_stride):
+        self.lib.check(self.lib.load().nve_layer_lookup(
+            self.layer, self.ctx, keys.size, ctypes.c_void_p(keys.ctypes.data), ctypes.c_void_p(out.ctypes.data),
+            out_stride, None, None))
+
+    def close(self):
+        self.lib.call("nve_context_destroy", self.ctx)
+        self.lib.call("nve_layer_destroy", self.layer)
+        self.lib.call("nve_table_destroy", self.t)
+        self.lib.call("nve_thread_pool_destroy", self.pool)
+
+
+def time_batches(run, batches, seconds, min_batches=20):
+    """3 untimed batches, then batches until `seconds` have passed and at least
+    `min_batches` ran; per-batch wall times (s), sorted."""
+    for i in range(3):
+        run(batches[i % len(batches)])
+    times, t0 = [], time.perf_counter()
+    while len(times) < min_batches or time.perf_counter() - t0 < seconds:
+        b = batches[len(times) % len(batches)]
+        t1 = time.perf_counter()
+        run(b)
+        times.append(time.perf_counter() - t1)
+    return sorted(times)
+
+
+def quantiles(ts):
+    n = len(ts)
+    return ts[n // 2], ts[max(0, int(0.1 * n))], ts[min(n - 1, int(0.9 * n))]
+
+
+def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, seconds, what):
+    """The product HostLayer timed on this host's cores on whole batches of the
+    workload: the reference's default worker count max(cores - 2, 1)
+    (thread_pool.cpp:112-116) for `value`, and every core beside it; median
+    batch time with p10 / p90 (at least 20 batches after 3 warm-up ones)."""
     model, avail = cpu_info()
-    threads = max(avail - 2, 1)  # SimpleThreadPool default (thread_pool.cpp:112-116)
-    log(f"cpu baseline: copying the table to host ({rows} x {dim} fp16)")
-    h_table = d_table.view(torch.int16).cpu().numpy().view(np.uint8).reshape(-1)
-    keys = [k.cpu().numpy() for k in key_batches]
-    # one warm-up batch, then whole batches until `seconds` of work
-    O.host_layer_lookup(keys[0], h_table, rows, dim * 2, O.F16, O.SUM, O.FIXED, None, bags, hot,
-                        None, 0, O.F16, threads)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        O.host_layer_lookup(keys[done % len(keys)], h_table, rows, dim * 2, O.F16, O.SUM, O.FIXED,
-                            None, bags, hot, None, 0, O.F16, threads)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and done >= 3:
-            break
-    n = keys[0].size
-    return {"value": done * n / el, "unit": "lookups/s", "cores": threads, "kind": "port",
-            "sample": f"{done} full batches of {n} keys (Fixed {hot} x {bags} bags, Sum, fp16) "
-                      f"in {el:.1f} s on '{model}' ({avail} cores available, {threads} worker threads)"}
+    n = key_batches[0].size
+    res = {}
+    for label, threads in (("default", max(avail - 2, 1)), ("all_cores", avail)):
+        base = HostLayerBaseline(lib, h_table, rows, row_bytes, dtype, threads)
+        try:
+            ts = time_batches(lambda k: run_batch(base, k), key_batches, seconds)
+        finally:
+            base.close()
+        med, p10, p90 = quantiles(ts)
+        res[label] = {"threads": threads, "batches": len(ts), "median_ms": round(med * 1e3, 3),
+                      "p10_ms": round(p10 * 1e3, 3), "p90_ms": round(p90 * 1e3, 3),
+                      "lookups_per_s": round(n / med, 1)}
+        log(f"cpu baseline ({label}, {threads} threads): median {med * 1e3:.2f} ms per {n}-key batch "
+            f"(p10 {p10 * 1e3:.2f}, p90 {p90 * 1e3:.2f}) = {n / med / 1e6:.1f} M lookups/s")
+    d = res["default"]
+    return {"value": d["lookups_per_s"], "unit": "lookups/s", "cores": d["threads"], "kind": "port",
+            "sample": f"{d['batches']} whole batches of {n} keys ({what}), median batch time, on '{model}' "
+                      f"({avail} cores available): the product HostLayer (libnve_amd.so, CPU threads)",
+            "median_ms": d["median_ms"], "p10_ms": d["p10_ms"], "p90_ms": d["p90_ms"],
+            "all_cores": res["all_cores"]}
 
 
 def read_ceiling(torch, lib, stream, counts):
@@ -231,7 +290,8 @@ def quant_rows_e4m3(torch, n, gen):
 
 def run_workload(args, torch, _lib):
     """Parity-test configurations of BASELINE.json measured the same way
-    (not the contract line): c2 (dedup then gather), c4a / c4b (dequant),
+    (not the contract line): c1 (the HostLayer configuration, GPU layer and
+    CPU HostLayer side by side), c2 (dedup then gather), c4a / c4b (dequant),
     c5 (26-table jagged weighted mean), c3 (LinearUVM cache over a host
     table) and c2bwd (training backprop of the c2pool lookup)."""
     L = _lib.load()
@@ -241,7 +301,84 @@ def run_workload(args, torch, _lib):
     kgen = torch.Generator(device="cuda")
     kgen.manual_seed(1)
     cfg_out = {"workload": w}
-    if w in ("c2", "c4a", "c4b"):
+    extra = {}
+    if w == "c1":
+        # BASELINE C1, the reference HostLayer configuration: 1,000,000 x 64 fp32
+        # N(0, 0.01); 4,096 bags of 8 keys uniform in [0, 1e6); the Fixed-8 Sum
+        # (the metric's find-and-pool) and the plain gather, on the GPU layer and
+        # on the product HostLayer beside it
+        import numpy as np
+        rows, dim, bags, hot = 1_000_000, 64, 4096, 8
+        nkeys, width = bags * hot, dim * 4
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0)
+        table = torch.empty((rows, dim), dtype=torch.float32, device="cuda").normal_(0.0, 0.01, generator=gen)
+        batches = [torch.randint(0, rows, (nkeys,), device="cuda", generator=kgen, dtype=torch.int64)
+                   for _ in range(args.batches)]
+        pooled = torch.empty((bags, dim), dtype=torch.float32, device="cuda")
+        gathered = torch.empty((nkeys, dim), dtype=torch.float32, device="cuda")
+        lc = L.nve_gpu_embedding_layer_config_default()
+        lc.layer_name = b"bench"
+        lc.embedding_table = table.data_ptr()
+        lc.num_embeddings = rows
+        lc.embedding_width_in_bytes = width
+        lc.value_dtype = _lib.DT_F32
+        layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.call("nve_gpu_embedding_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), None)
+        _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
+        kp = [ctypes.c_void_p(b.data_ptr()) for b in batches]
+
+        def step(i):
+            _lib.check(L.nve_layer_lookup_pooled(layer, ctx, nkeys, kp[i % len(kp)], ctypes.c_void_p(pooled.data_ptr()),
+                                                 width, None, _lib.POOL_SUM, _lib.SPARSE_FIXED, None, 0, hot, None,
+                                                 _lib.DT_UNKNOWN, _lib.DT_F32, None))
+
+        def plain(i):
+            _lib.check(L.nve_layer_lookup(layer, ctx, nkeys, kp[i % len(kp)], ctypes.c_void_p(gathered.data_ptr()),
+                                          width, None, None))
+
+        ms_plain = time_steps(torch, stream, plain, args.warmup, args.steps)
+        ms = time_steps(torch, stream, step, args.warmup, args.steps)
+        extra["step_spread"] = step_spread(torch, stream, step)
+        # untimed: the last pooled batch against torch's float64 sums, the gather bitwise
+        step(0)
+        plain(0)
+        torch.cuda.synchronize()
+        ref = table[batches[0]].double().view(bags, hot, dim).sum(1)
+        if not torch.allclose(pooled.double(), ref, rtol=1e-5, atol=1e-7):
+            raise SystemExit("bench.py: c1 pooled output differs from its float64 sums")
+        if not torch.equal(gathered, table[batches[0]]):
+            raise SystemExit("bench.py: c1 gathered rows differ from the table rows")
+        _lib.call("nve_context_wait", ctx)
+        _lib.call("nve_context_destroy", ctx)
+        _lib.call("nve_layer_destroy", layer)
+        alg = nkeys * 8 + nkeys * width + bags * width
+        alg_plain = nkeys * 8 + 2 * nkeys * width
+        cfg_out.update({"table_rows": rows, "dim": dim, "row_dtype": "f32", "bags": bags, "hotness": hot,
+                        "keys": "uniform", "pooling": "sum", "output_dtype": "f32",
+                        "plain_gather_ms": round(ms_plain, 6),
+                        "plain_gather_lookups_per_s": round(nkeys / (ms_plain * 1e-3), 1),
+                        "plain_gather_GBps": round(alg_plain / (ms_plain * 1e-3) / 1e9, 1)})
+        kernel = "pool_short_kernel (Fixed 8, one lane group per bag)"
+        if not args.no_cpu:
+            h_table = table.cpu().numpy().view(np.uint8).reshape(-1)
+            h_keys = [b.cpu().numpy() for b in batches[:8]]
+            h_pooled = np.empty((bags, dim), np.float32)
+            h_gathered = np.empty((nkeys, dim), np.float32)
+            extra["cpu_baseline"] = cpu_baseline(
+                _lib, h_table, rows, width, _lib.DT_F32, h_keys,
+                lambda base, k: base.pooled(k, h_pooled, width, hot, _lib.DT_F32), args.cpu_seconds,
+                f"Fixed {hot} x {bags} bags, Sum, fp32")
+            gb = HostLayerBaseline(_lib, h_table, rows, width, _lib.DT_F32, max(cpu_info()[1] - 2, 1))
+            try:
+                ts = time_batches(lambda k: gb.gather(k, h_gathered, width), h_keys, args.cpu_seconds / 2)
+            finally:
+                gb.close()
+            med, p10, p90 = quantiles(ts)
+            extra["cpu_baseline"]["plain_gather"] = {"median_ms": round(med * 1e3, 3), "p10_ms": round(p10 * 1e3, 3),
+                                                     "p90_ms": round(p90 * 1e3, 3),
+                                                     "lookups_per_s": round(nkeys / med, 1)}
+    elif w in ("c2", "c4a", "c4b"):
         if w == "c2":
             rows, width, nkeys, alpha = 50_000_000, 256, 262144, 1.05
             gen = torch.Generator(device="cuda")
@@ -521,6 +658,7 @@ def run_workload(args, torch, _lib):
            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                         "kernel": kernel, "alg_bytes_per_launch": alg}}
+    res.update(extra)
     log(f"{w}: {ms * 1000:.2f} us/step, {res['value'] / 1e9:.2f} G lookups/s, {achieved:.0f} GB/s")
     print(json.dumps(res), flush=True)
 
@@ -528,7 +666,7 @@ def run_workload(args, torch, _lib):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="c2pool",
-                    choices=["c2pool", "c2", "c2bwd", "c3", "c4a", "c4b", "c5"],
+                    choices=["c2pool", "c1", "c2", "c2bwd", "c3", "c4a", "c4b", "c5"],
                     help="c2pool (default, the metric's configuration) or a parity configuration")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -539,7 +677,8 @@ def main():
     ap.add_argument("--hotness", type=int, default=1024)
     ap.add_argument("--alpha", type=float, default=1.05)
     ap.add_argument("--batches", type=int, default=16, help="distinct key batches cycled")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0,
+                    help="CPU baseline: seconds of batches per thread setting")
     # BASELINE's C3 is 400M rows (102.4 GB pinned) with a 32 GB cache; the GPU
     # boxes pin at most ~64-80 GiB per allocation, so the default keeps the
     # table:cache ratio at 256M rows (65.5 GB) and a 20 GiB cache
@@ -693,9 +832,18 @@ def main():
                              "random_row_read_GBps_4x_rows": round(c4, 1),
                              "frac_of_4x_rows_ceiling": round(achieved / c4, 4)}
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(torch, d_table, batches[:4], bags, hot, rows, dim,
-                                              args.cpu_seconds)
-        result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 1)
+        import numpy as np
+        log(f"cpu baseline: copying the table to host ({rows} x {dim} fp16)")
+        h_table = d_table.view(torch.int16).cpu().numpy().view(np.uint8).reshape(-1)
+        h_keys = [b.cpu().numpy() for b in batches[:4]]
+        h_out = np.empty((bags, dim), np.float16)
+
+        def run_batch(base, k):
+            base.pooled(k, h_out, width, hot, _lib.DT_F16)
+
+        result["cpu_baseline"] = cpu_baseline(_lib, h_table, rows, width, _lib.DT_F16, h_keys, run_batch,
+                                              args.cpu_seconds, f"Fixed {hot} x {bags} bags, Sum, fp16")
+        del h_table
     _lib.call("nve_context_wait", ctx)
     _lib.call("nve_context_destroy", ctx)
     _lib.call("nve_layer_destroy", layer)
