@@ -88,6 +88,20 @@ NVE_C_API nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num
                                             int64_t output_stride, void* workspace,
                                             uint64_t workspace_bytes, void* stream);
 
+/* nve_amd_dedup_gather without the workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it has no counterpart in the reference.  It allocates
+ * nothing: its scratch is a fixed 16 MiB device array, one per GPU, held
+ * until the process ends.  num_keys must not exceed 262,144 (larger batches
+ * fail with NVE_ERROR_INVALID_ARGUMENT).  Every call on one GPU uses that
+ * GPU's array, so calls that overlap on one GPU (two streams, two threads)
+ * race and must be serialized by the caller.  Same results as
+ * nve_amd_dedup_gather; asynchronous on `stream`. */
+NVE_C_API nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_keys,
+                                                    const void* keys, const void* table,
+                                                    int64_t num_rows, int64_t row_size_in_bytes,
+                                                    void* output, int64_t output_stride, void* stream);
+
 /* Random-row read ceiling microbenchmark: reads row idx[i] (row_size_in_bytes
  * each, a multiple of 16) of a device table for i < n and folds the bytes into
  * sink (one uint32 per 256-thread workgroup, ceil(n/128) words). */

@@ -12,6 +12,7 @@
 #include "backprop.hpp"
 #include "dedup.hpp"
 #include "host_layer.hpp"
+#include "kernels/noalloc_launch.hpp"
 #include "layers.hpp"
 
 using namespace nve_amd;
@@ -921,6 +922,27 @@ nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num_keys, con
   dedup_gather_run(key_bytes_of(key_type), num_keys, keys, static_cast<const uint8_t*>(table),
                    num_rows, row_size_in_bytes, output, output_stride, workspace, workspace_bytes,
                    (hipStream_t)stream);
+  return NVE_SUCCESS;
+  C_CATCH
+}
+
+nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_keys, const void* keys,
+                                          const void* table, int64_t num_rows, int64_t row_size_in_bytes,
+                                          void* output, int64_t output_stride, void* stream) {
+  C_TRY
+  NVE_CHECK_ARG(num_keys >= 0 && num_keys <= kNoAllocMaxKeys, "num_keys must be in [0, ", kNoAllocMaxKeys,
+                "] for the allocation-free dedup gather (got ", num_keys, ")");
+  NVE_CHECK_ARG(num_rows > 0 && row_size_in_bytes > 0, "Invalid table shape");
+  NVE_CHECK_ARG(output_stride >= row_size_in_bytes, "output_stride is smaller than a row");
+  if (num_keys == 0) return NVE_SUCCESS;
+  NVE_CHECK_ARG(keys && table && output, "keys, table and output must not be NULL");
+  const size_t need = dedup_workspace_bytes(num_keys);
+  NVE_CHECK(need <= kNoAllocScratchBytes, "The device scratch (", kNoAllocScratchBytes,
+            " bytes) is smaller than the dedup workspace of ", num_keys, " keys (", need, " bytes)");
+  void* ws = nullptr;
+  NVE_HIP(noalloc_scratch(&ws));
+  dedup_gather_run(key_bytes_of(key_type), num_keys, keys, static_cast<const uint8_t*>(table), num_rows,
+                   row_size_in_bytes, output, output_stride, ws, need, (hipStream_t)stream);
   return NVE_SUCCESS;
   C_CATCH
 }

@@ -147,6 +147,7 @@ SIGNATURES = {
     "nve_amd_dedup_workspace_size": (I32, [I64, ctypes.POINTER(U64)]),
     "nve_amd_dedup": (I32, [ctypes.c_int, I64, P, P, P, P, P, PI64, P, U64, P]),
     "nve_amd_dedup_gather": (I32, [ctypes.c_int, I64, P, P, I64, I64, P, I64, P, U64, P]),
+    "nve_amd_dedup_gather_noalloc": (I32, [ctypes.c_int, I64, P, P, I64, I64, P, I64, P]),
     "nve_amd_gpu_table_num_sets": (I32, [P, PI64]),
     "nve_amd_gpu_table_export_state": (I32, [P, P, P, P, PI64]),
     "nve_amd_gpu_table_import_state": (I32, [P, P, P, P, I64]),
