@@ -50,6 +50,32 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   __builtin_memcpy(&h, &x, 2);
   return h;
 }
+// acc + float(h) (lo: the low half of w, hi: the high half) and
+// fma(float(h), wt, acc) as one v_fma_mix_f32 each: the half is widened inside
+// the instruction (exactly) and the result rounded once to binary32, so the
+// bits are those of the widen-then-add / widen-then-fma pair it replaces
+// (h * 1.0 is exact).  One VALU instruction per element instead of two.
+__device__ __forceinline__ float acc_half_lo(float acc, uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(acc));
+  return r;
+}
+__device__ __forceinline__ float acc_half_hi(float acc, uint32_t w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(acc));
+  return r;
+}
+__device__ __forceinline__ float fma_half_lo(uint32_t w, float wt, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(wt), "v"(acc));
+  return r;
+}
+__device__ __forceinline__ float fma_half_hi(uint32_t w, float wt, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(wt), "v"(acc));
+  return r;
+}
+
 // OCP FP8 E4M3FN (bias 7, no infinities, NaN = S.1111.111), decoded exactly.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
   const uint32_t s = (v & 0x80u) << 24;

@@ -16,9 +16,11 @@ namespace nve_amd {
 constexpr int kDppRowNewBcast = 0x150;  // + n: every lane of a row reads lane n of that row
 constexpr int kDppRowRor8 = 0x128;      // lane l reads lane (l + 8) mod 16 of its row: l ^ 8
 
+// Every row and bank enabled and every source lane inside the wave, so each
+// lane is written and no "old" value is needed.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
 }
 
 // Value of lane J of this lane's G-lane group (groups aligned to G lanes);

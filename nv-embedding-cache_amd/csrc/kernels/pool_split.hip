@@ -73,6 +73,37 @@ __device__ __forceinline__ void butterfly(float* acc, int e, float& wsum, bool w
   }
 }
 
+// acc += row, or acc = fma(row, wt, acc) when weighted, for one 16-byte slice
+// of a stored f16 / f32 row.  f16 slices accumulate with one v_fma_mix_f32 per
+// element (same bits as widening then adding).  A lane with nothing to add
+// has loaded the zero row: adding +0 leaves acc unchanged (acc starts at +0
+// and a round-to-nearest sum is -0 only when both terms are), so the
+// unweighted sum needs no select; weighted callers pass wt = 0 for such a
+// lane (0 * 0 + acc), which also keeps a non-finite weight of a key outside
+// the table out of the sum.
+template <int SDT, int E, bool W>
+__device__ __forceinline__ void add_slice(float (&acc)[E], const Vec<16>& v, float wt) {
+  if constexpr (SDT == kF16) {
+#pragma unroll
+    for (int c = 0; c < E / 2; ++c) {
+      if constexpr (W) {
+        acc[2 * c] = fma_half_lo(v.w[c], wt, acc[2 * c]);
+        acc[2 * c + 1] = fma_half_hi(v.w[c], wt, acc[2 * c + 1]);
+      } else {
+        acc[2 * c] = acc_half_lo(acc[2 * c], v.w[c]);
+        acc[2 * c + 1] = acc_half_hi(acc[2 * c + 1], v.w[c]);
+      }
+    }
+  } else {
+    static_assert(SDT == kF32, "f16 or f32 rows");
+#pragma unroll
+    for (int c = 0; c < E; ++c) {
+      const float x = __uint_as_float(v.w[c]);
+      acc[c] = W ? __builtin_fmaf(x, wt, acc[c]) : acc[c] + x;
+    }
+  }
+}
+
 // The kernel's arguments: only what this shape reads (PoolLaunch carries a
 // table array for multi-table launches; a smaller kernarg segment is quicker
 // to set up per launch).
@@ -198,6 +229,7 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(
   const uint64_t row_bytes = a.row_bytes;
   const uint64_t num_rows = a.num_rows;
   const uint64_t zero_row = (uint64_t)g_zero_row;
+  const uint32_t rb32 = (uint32_t)row_bytes;  // launcher: row_bytes < 2^32, off < the zero row's size
   const int64_t value_bytes = a.count * ES;
   const int off = gl * VB;
   const bool in_row = off < value_bytes;
@@ -237,30 +269,26 @@ __global__ __launch_bounds__(1024) void pool_split_kernel(
       Vec<VB> v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        // base and row index picked by selects (no divergent branch), then one
+        // 32 x 32 -> 64-bit multiply-add: row_bytes < 2^32
+        // one 32 x 32 -> 64-bit multiply-add per address (row_bytes < 2^32);
+        // select-based addressing (base and index picked per lane) measured
+        // slower than this form on both bag shapes
         const bool real = ri[u] != kNoRow && in_row;
         uint64_t base;
         if constexpr (CACHE) {
-          base = (ri[u] & kBackingRow) ? table + (uint64_t)(ri[u] & ~kBackingRow) * row_bytes
-                                       : (uint64_t)a.cache_data + (uint64_t)ri[u] * row_bytes;
+          base = (ri[u] & kBackingRow) ? table + (uint64_t)(ri[u] & ~kBackingRow) * rb32
+                                       : (uint64_t)a.cache_data + (uint64_t)ri[u] * rb32;
         } else {
-          base = table + (uint64_t)ri[u] * row_bytes;
+          base = table + (uint64_t)ri[u] * rb32;
         }
-        const uint64_t addr = real ? base + (uint64_t)off : zero_row + (uint64_t)(off & kZeroRowMask);
-        v[u] = load_vec<VB>(addr);
+        v[u] = load_vec<VB>(real ? base + (uint64_t)off : zero_row + (uint64_t)off);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool use = j0 + u < n;  // uniform over the group
         if (W && use) wsum += wu[u];
-        const bool add = use && in_row && ri[u] != kNoRow;
-        float x[E];
-        Meta m{1.0f, 0.0f};
-        decode<SDT, VB>(v[u], m, x);
-#pragma unroll
-        for (int c = 0; c < E; ++c) {
-          const float t = W ? __builtin_fmaf(x[c], wu[u], acc[c]) : acc[c] + x[c];
-          acc[c] = add ? t : acc[c];
-        }
+        add_slice<SDT, E, W>(acc, v[u], (use && in_row && ri[u] != kNoRow) ? wu[u] : 0.0f);
       }
     };
     for_batches<U, 0, G / U>(batch);
@@ -434,9 +462,9 @@ __global__ __launch_bounds__(256) void pool_short_kernel(std::conditional_t<MT, 
   } else {
     out_row += bag * a.out_stride;
   }
-  const uint64_t row_bytes = a.row_bytes;
+  const uint32_t rb32 = (uint32_t)a.row_bytes;  // launcher: row_bytes < 2^32
   const uint64_t zero_row = (uint64_t)g_zero_row;
-  const int off = gl * VB;
+  const int off = gl * VB;  // < the zero row's size: one pass covers the row
   const bool in_row = off < a.count * ES;
 
   float acc[E];
@@ -464,23 +492,13 @@ __global__ __launch_bounds__(256) void pool_short_kernel(std::conditional_t<MT, 
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool real = ri[u] != kNoRow && in_row;
-        const uint64_t addr = real ? table + (uint64_t)ri[u] * row_bytes + (uint64_t)off
-                                   : zero_row + (uint64_t)(off & kZeroRowMask);
-        v[u] = load_vec<VB>(addr);
+        v[u] = load_vec<VB>(real ? table + (uint64_t)ri[u] * rb32 + (uint64_t)off : zero_row + (uint64_t)off);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool use = j0 + u < n;
         if (W && use) wsum += wu[u];
-        const bool add = use && in_row && ri[u] != kNoRow;
-        float x[E];
-        Meta m{1.0f, 0.0f};
-        decode<SDT, VB>(v[u], m, x);
-#pragma unroll
-        for (int c = 0; c < E; ++c) {
-          const float t = W ? __builtin_fmaf(x[c], wu[u], acc[c]) : acc[c] + x[c];
-          acc[c] = add ? t : acc[c];
-        }
+        add_slice<SDT, E, W>(acc, v[u], (use && in_row && ri[u] != kNoRow) ? wu[u] : 0.0f);
       }
     };
     for_batches<U, 0, G / U>(batch);
@@ -566,6 +584,7 @@ bool pool_short_eligible(const PoolLaunch& a, const PoolGeometry& g) {
   if (a.src.cache_data != nullptr || !a.src.load_indices) return false;
   if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
   if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;
+  if (a.src.row_bytes == 0 || a.src.row_bytes > 0xffffffffull) return false;  // 32-bit row stride
   if (g.vb != 16 || g.passes != 1 || g.gpb != 1 || g.g < 8 || g.g > 64) return false;
   if (a.num_tables > 0) {
     for (int t = 0; t < a.num_tables; ++t)
@@ -597,6 +616,7 @@ bool pool_split_eligible(const PoolLaunch& a, const PoolGeometry& g) {
   }
   if (a.stored_dtype != kF16 && a.stored_dtype != kF32) return false;
   if (a.out_dtype != kF16 && a.out_dtype != kF32) return false;
+  if (a.src.row_bytes == 0 || a.src.row_bytes > 0xffffffffull) return false;  // 32-bit row stride
   if (g.vb != 16 || g.passes != 1 || g.bags_per_wg != 1) return false;
   if (g.g < 8 || g.g > 64 || g.gpb * g.g <= 64 || g.gpb * g.g > 1024) return false;
   if (g.threads != g.gpb * g.g) return false;
