@@ -439,7 +439,7 @@ def run_workload(args, torch, _lib):
         _lib.call("nve_context_wait", ctx)
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
-        kernel = "sort + gather_kernel" if w == "c2" else "gather_kernel (dequant)"
+        kernel = "sort + gather_kernel" if w == "c2" else "gather_realign_kernel (dequant)"
     elif w == "c3":
         # LinearUVM: pinned host table + 32 GiB 8-way HBM cache, warmed by 10
         # batches (auto-insert), then timed pooled lookups whose misses read the
@@ -658,9 +658,28 @@ def run_workload(args, torch, _lib):
            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                         "kernel": kernel, "alg_bytes_per_launch": alg}}
+    add_traffic(res["roofline"], w, ms)
     res.update(extra)
     log(f"{w}: {ms * 1000:.2f} us/step, {res['value'] / 1e9:.2f} G lookups/s, {achieved:.0f} GB/s")
     print(json.dumps(res), flush=True)
+
+
+def add_traffic(roof, workload, ms):
+    """HBM bytes per launch of the workload's dominant kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json), over this
+    run's time per step: the HBM rate net of L2 / MALL reuse."""
+    tf = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(tf):
+        return
+    with open(tf) as f:
+        entry = json.load(f).get(workload)
+    if not entry:
+        return
+    roof["traffic"] = entry["traffic_bytes_per_launch"]
+    dram = roof["traffic"] / (ms * 1e-3) / 1e9
+    roof["achieved_dram"] = round(dram, 1)
+    roof["frac_dram"] = round(dram / HBM_PEAK_GBPS, 4)
+    roof["traffic_source"] = entry["profile"] + " (rocprofv3 --pmc)"
 
 
 def main():
@@ -795,17 +814,7 @@ def main():
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
             "kernel": "pool_split_kernel<F16, G=16, unweighted>", "alg_bytes_per_launch": alg}
-    tf = os.path.join(ROOT, "profiles", "c2pool_traffic.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            roof["traffic"] = json.load(f).get("traffic_bytes_per_launch")
-    if roof["traffic"]:
-        # DRAM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel and workload, committed
-        # profile) over this run's kernel time: the HBM fraction net of L2 / MALL reuse
-        dram = roof["traffic"] / (ms * 1e-3) / 1e9
-        roof["achieved_dram"] = round(dram, 1)
-        roof["frac_dram"] = round(dram / HBM_PEAK_GBPS, 4)
-        roof["traffic_source"] = "profiles/pool_split_kernel_c2pool_traffic.md (rocprofv3 --pmc)"
+    add_traffic(roof, "c2pool", ms)
     result = {"metric": METRIC, "value": round(nkeys / (ms * 1e-3), 1), "unit": "lookups/s",
               "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",

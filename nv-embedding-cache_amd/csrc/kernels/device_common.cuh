@@ -44,7 +44,11 @@ __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)x;
 }
 // binary32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default mode).
+// The empty asm keeps the binary32 value as it is: without it the compiler may
+// fold a conversion of an fma or product into one v_fma_mixlo_f16, which
+// rounds once to binary16 where the formulas round to binary32 first.
 __device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
   _Float16 x = (_Float16)f;
   uint16_t h;
   __builtin_memcpy(&h, &x, 2);
@@ -76,21 +80,31 @@ __device__ __forceinline__ float fma_half_hi(uint32_t w, float wt, float acc) {
   return r;
 }
 
-// OCP FP8 E4M3FN (bias 7, no infinities, NaN = S.1111.111), decoded exactly.
+// OCP FP8 E4M3FN (bias 7, no infinities, NaN = S.1111.111), decoded exactly
+// and without branches: a normal code E.M becomes exponent E + 120, mantissa
+// M << 20, i.e. (code << 20) + (120 << 23); a subnormal code (E = 0) is
+// M * 2^-9, exact in binary32; S.1111.111 is the quiet NaN with the code's sign.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t v) {
-  const uint32_t s = (v & 0x80u) << 24;
-  const uint32_t e = (v >> 3) & 0xfu;
-  const uint32_t m = v & 7u;
-  uint32_t bits;
-  if (e == 0) {
-    // m * 2^-9 is exact in binary32
-    return __uint_as_float(s | __float_as_uint((float)m * 0.001953125f));
-  } else if (e == 15 && m == 7) {
-    bits = s | 0x7fc00000u;
-  } else {
-    bits = s | ((e + 120u) << 23) | (m << 20);
-  }
-  return __uint_as_float(bits);
+  const uint32_t a = v & 0x7fu;
+  const uint32_t sub = __float_as_uint((float)a * 0.001953125f);
+  uint32_t bits = a < 8u ? sub : (a << 20) + (120u << 23);
+  bits = a == 0x7fu ? 0x7fc00000u : bits;
+  return __uint_as_float(((v & 0x80u) << 24) | bits);
+}
+
+// The four E4M3 codes of w (byte k = value k) through gfx950's packed
+// conversion, two codes per instruction.  It gives e4m3_to_f32's bits for
+// every code except 0.1111.111, the positive NaN, which it returns with the
+// sign bit set; putting each code's own sign bit back (one bitfield insert per
+// value) makes all 256 codes agree.
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float (&x)[4]) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);  // bytes 0 and 1
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);   // bytes 2 and 3
+  const uint32_t r[4] = {__float_as_uint(lo[0]), __float_as_uint(lo[1]), __float_as_uint(hi[0]),
+                         __float_as_uint(hi[1])};
+  const uint32_t sign[4] = {w << 24, w << 16, w << 8, w};  // byte k's top bit at bit 31
+#pragma unroll
+  for (int k = 0; k < 4; ++k) x[k] = __uint_as_float((r[k] & 0x7fffffffu) | (sign[k] & 0x80000000u));
 }
 
 // ---------------------------------------------------------------------------
@@ -155,14 +169,22 @@ __device__ __forceinline__ uint16_t vhalf(const uint32_t* w, int e) {
   return (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
 }
 
-// Streaming store (the output is written once and not re-read by the lookup).
-template <int VB>
+// NT: streaming (nontemporal) store, the output being written once and not
+// re-read by the lookup; otherwise an ordinary store.  Measured per kernel:
+// the dequantizing gather's 1 KiB fp32 rows write faster as ordinary stores
+// (C4b 32.2 -> 28.7 us), the pooled and plain gathers slightly faster as
+// streaming stores.
+template <int VB, bool NT = true>
 __device__ __forceinline__ void store_vec(uint8_t* p, const Vec<VB>& v) {
   const uint64_t a = (uint64_t)p;
   if constexpr (VB >= 4) {
 #pragma unroll
-    for (int i = 0; i < VB / 4; ++i)
-      __builtin_nontemporal_store(v.w[i], reinterpret_cast<gptr_w<uint32_t>>(a) + i);
+    for (int i = 0; i < VB / 4; ++i) {
+      if constexpr (NT)
+        __builtin_nontemporal_store(v.w[i], reinterpret_cast<gptr_w<uint32_t>>(a) + i);
+      else
+        reinterpret_cast<gptr_w<uint32_t>>(a)[i] = v.w[i];
+    }
   } else if constexpr (VB == 2) {
     *reinterpret_cast<gptr_w<uint16_t>>(a) = (uint16_t)v.w[0];
   } else {
@@ -171,7 +193,7 @@ __device__ __forceinline__ void store_vec(uint8_t* p, const Vec<VB>& v) {
 }
 
 // Store E floats (as f32 or RNE f16) at p, which is aligned to E*element bytes.
-template <int E>
+template <int E, bool NT = true>
 __device__ __forceinline__ void store_out(uint8_t* p, const float* v, bool out_f16) {
   if (out_f16) {
     Vec<2 * E> o;
@@ -182,20 +204,20 @@ __device__ __forceinline__ void store_out(uint8_t* p, const float* v, bool out_f
       for (int i = 0; i < E / 2; ++i)
         o.w[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
     }
-    store_vec<2 * E>(p, o);
+    store_vec<2 * E, NT>(p, o);
   } else {
     if constexpr (E <= 4) {
       Vec<4 * E> o;
 #pragma unroll
       for (int i = 0; i < E; ++i) o.w[i] = __float_as_uint(v[i]);
-      store_vec<4 * E>(p, o);
+      store_vec<4 * E, NT>(p, o);
     } else {
 #pragma unroll
       for (int c = 0; c < E / 4; ++c) {
         Vec<16> o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint(v[4 * c + i]);
-        store_vec<16>(p + 16 * c, o);
+        store_vec<16, NT>(p + 16 * c, o);
       }
     }
   }
@@ -324,7 +346,16 @@ __device__ __forceinline__ void decode(const Vec<VB>& v, const Meta& m,
     } else if constexpr (SDT == kQU8F16) {
       x[e] = h2f(f2h(__builtin_fmaf((float)vbyte(v.w, e), m.s, m.o)));
     } else if constexpr (SDT == kXE4M3F32) {
-      x[e] = e4m3_to_f32((uint8_t)vbyte(v.w, e)) * m.s;
+      if constexpr (VB >= 4) {
+        if (e % 4 == 0) {
+          float q[4];
+          e4m3x4_to_f32(v.w[e / 4], q);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) x[e + k] = q[k] * m.s;
+        }
+      } else {
+        x[e] = e4m3_to_f32((uint8_t)vbyte(v.w, e)) * m.s;
+      }
     }
   }
 }

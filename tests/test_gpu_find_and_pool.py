@@ -146,6 +146,11 @@ def test_e4m3_every_code_decodes_exactly():
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # NaN codes included, bit for bit with the oracle: S.1111.111 decodes to
+    # the quiet NaN with the code's sign (S = 0 and S = 1 both)
+    orc = oracle_dequant(tb, keys, O.XE4M3_F32, count, O.F32).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), orc.view(np.uint32))
+    assert got.view(np.uint32)[0x7F] == 0x7FC00000 and got.view(np.uint32)[0xFF] == 0xFFC00000
 
 
 @pytest.mark.parametrize("dtype", [O.F16, O.XI8A_F32])
