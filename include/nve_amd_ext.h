@@ -162,9 +162,11 @@ NVE_C_API nve_status_t nve_amd_linear_host_table_create(nve_table_t* out, nve_ke
  * w / (the bag's weights added in order).  Outputs: the unique keys ascending
  * (reserve num_keys entries of the key type), one gradient row per unique key
  * (reserve num_keys rows) and *num_unique_out.  Sums are fp32 in a fixed order
- * (each key's positions in runs of 64, then the runs) and rounded once, so the
- * result is deterministic.  Device buffers and workspace; synchronizes the
- * stream. */
+ * and rounded once, so the result is deterministic: the positions in dedup
+ * order are cut into blocks of 32, each key's positions inside one block are
+ * added in position order, and a key's J block sums are added in 8
+ * consecutive sub-sequences of ceil(J / 8), then the 8 sub-sums in order.
+ * Device buffers and workspace; synchronizes the stream. */
 NVE_C_API nve_status_t nve_amd_backprop_workspace_size(int64_t num_keys, int64_t num_bags,
                                                        int64_t embedding_width, uint64_t* bytes);
 NVE_C_API nve_status_t nve_amd_pooling_backprop(

@@ -407,9 +407,11 @@ nve_status_t nve_table_create_execution_context(nve_table_t table, nve_context_t
         (hipStream_t)lookup_stream, (hipStream_t)modify_stream, unwrap(thread_pool))};
     return NVE_SUCCESS;
   }
-  *out = new nve_context_s{std::make_shared<ExecutionContext>(
-      table->ptr->config().device_id, (hipStream_t)lookup_stream, (hipStream_t)modify_stream,
-      unwrap(thread_pool))};
+  auto ctx = std::make_shared<ExecutionContext>(table->ptr->config().device_id,
+                                                (hipStream_t)lookup_stream,
+                                                (hipStream_t)modify_stream, unwrap(thread_pool));
+  ctx->watch(table->ptr->lookup_streams());
+  *out = new nve_context_s{std::move(ctx)};
   return NVE_SUCCESS;
   C_CATCH
 }

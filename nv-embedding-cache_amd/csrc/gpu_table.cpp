@@ -25,6 +25,7 @@ uint64_t align16(uint64_t x) { return (x + 15) / 16 * 16; }
 
 GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_bytes), cfg_(cfg) {
   ScopedDevice sd(cfg_.device_id);
+  if (cfg_.private_stream) lookups_->add(cfg_.private_stream);  // lookups run there
   NVE_CHECK(key_bytes == 4 || key_bytes == 8, "Unsupported key size ", key_bytes);
   NVE_CHECK(cfg_.row_size_in_bytes > 0, "Invalid row size");
   NVE_CHECK(cfg_.uvm_table == nullptr || cfg_.uvm_num_rows > 0,
@@ -273,8 +274,7 @@ void GpuTable::clear(ExecutionContext& ctx) {
 
 void GpuTable::export_state(void* tags, float* counters, int64_t* set_ts, int64_t* global_ts) {
   ScopedDevice sd(cfg_.device_id);
-  std::lock_guard<std::mutex> mk(modify_mu_);
-  NVE_HIP(hipDeviceSynchronize());
+  std::lock_guard<std::mutex> mk(modify_mu_);  // modifies end with their stream synchronized
   const size_t ways = (size_t)num_sets_ * kWays;
   if (tags) NVE_HIP(hipMemcpy(tags, tags_, ways * key_bytes_, hipMemcpyDefault));
   if (cfg_.modify_on_gpu) {
@@ -292,20 +292,26 @@ void GpuTable::import_state(const void* tags, const float* counters, const int64
   ScopedDevice sd(cfg_.device_id);
   std::lock_guard<std::mutex> mk(modify_mu_);
   std::unique_lock<std::shared_mutex> lk(uvm_mu_);
-  NVE_HIP(hipDeviceSynchronize());
+  lookups_->drain();  // lookups queued so far read the old tags to the end
   const size_t ways = (size_t)num_sets_ * kWays;
-  if (tags) NVE_HIP(hipMemcpy(tags_, tags, ways * key_bytes_, hipMemcpyDefault));
+  // copies on the null stream, then waited for: a copy from pageable memory
+  // may still be in flight when hipMemcpy returns, and lookups queued after
+  // this call must see the imported state
+  const hipStream_t s = nullptr;
+  if (tags) NVE_HIP(hipMemcpyAsync(tags_, tags, ways * key_bytes_, hipMemcpyDefault, s));
   if (cfg_.modify_on_gpu) {
-    if (counters) NVE_HIP(hipMemcpy(counters_, counters, ways * sizeof(float), hipMemcpyDefault));
-    if (set_ts) NVE_HIP(hipMemcpy(set_ts_, set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+    if (counters)
+      NVE_HIP(hipMemcpyAsync(counters_, counters, ways * sizeof(float), hipMemcpyDefault, s));
+    if (set_ts)
+      NVE_HIP(hipMemcpyAsync(set_ts_, set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault, s));
   } else {
-    if (tags) NVE_HIP(hipMemcpy(h_tags_.data(), tags, ways * key_bytes_, hipMemcpyDefault));
-    if (counters) NVE_HIP(hipMemcpy(h_counters_.data(), counters, ways * sizeof(float), hipMemcpyDefault));
-    if (set_ts) NVE_HIP(hipMemcpy(h_set_ts_.data(), set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault));
+    if (tags) NVE_HIP(hipMemcpyAsync(h_tags_.data(), tags, ways * key_bytes_, hipMemcpyDefault, s));
+    if (counters)
+      NVE_HIP(hipMemcpyAsync(h_counters_.data(), counters, ways * sizeof(float), hipMemcpyDefault, s));
+    if (set_ts)
+      NVE_HIP(hipMemcpyAsync(h_set_ts_.data(), set_ts, num_sets_ * sizeof(int64_t), hipMemcpyDefault, s));
   }
-  // a copy from pageable memory may still be in flight when hipMemcpy returns;
-  // lookups on any stream after this call must see the imported state
-  NVE_HIP(hipDeviceSynchronize());
+  NVE_HIP(hipStreamSynchronize(s));
   global_ts_ = global_ts;
 }
 

@@ -94,8 +94,8 @@ void GpuTable::apply_records(ExecutionContext& ctx, hipStream_t s, const std::ve
   NVE_HIP(launch_invalidate(d_num, cnt, d_slot, tags_, key_bytes_, cfg_.invalid_key, s));
   NVE_HIP(hipStreamSynchronize(s));
   if (!invalidate_only) {
-    // lookups queued earlier on any stream finish before a row is overwritten
-    NVE_HIP(hipDeviceSynchronize());
+    // lookups queued before the invalidation finish before a row is overwritten
+    lookups_->order_before(s);
     uintptr_t align = 0;
     for (uint64_t p : src) align |= (uintptr_t)p;
     const int src_align = (align % 16 == 0) ? 16 : (align % 4 == 0) ? 4 : 1;

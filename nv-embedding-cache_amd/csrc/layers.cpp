@@ -69,7 +69,9 @@ void EmbeddingLayer::erase(ExecutionContext&, int64_t, const void*, int64_t) {
 
 std::shared_ptr<ExecutionContext> EmbeddingLayer::create_execution_context(
     hipStream_t lookup, hipStream_t modify, std::shared_ptr<ThreadPool> pool) {
-  return std::make_shared<ExecutionContext>(device_, lookup, modify, std::move(pool));
+  auto ctx = std::make_shared<ExecutionContext>(device_, lookup, modify, std::move(pool));
+  if (auto streams = lookup_streams()) ctx->watch(streams);
+  return ctx;
 }
 
 // ---------------------------------------------------------------------------

@@ -66,6 +66,9 @@ class EmbeddingLayer {
   virtual std::shared_ptr<ExecutionContext> create_execution_context(
       hipStream_t lookup, hipStream_t modify, std::shared_ptr<ThreadPool> pool);
   virtual int64_t num_tables() const { return 1; }
+  // the registry a context of this layer adds its lookup stream to (none: the
+  // layer's modifies need no lookup ordered before them)
+  virtual std::shared_ptr<LookupStreams> lookup_streams() const { return nullptr; }
 
   int key_bytes() const { return key_bytes_; }
   int device() const { return device_; }
@@ -106,10 +109,12 @@ class GPUEmbeddingLayer : public EmbeddingLayer {
   void clear(ExecutionContext& ctx) override;
   void erase(ExecutionContext& ctx, int64_t n, const void* keys, int64_t table_id) override;
   const GPUEmbeddingLayerConfig& config() const { return cfg_; }
+  std::shared_ptr<LookupStreams> lookup_streams() const override { return lookups_; }
 
  private:
   GPUEmbeddingLayerConfig cfg_;
   std::mutex launch_mu_;  // lookups are serialised like kernel_launch_mutex_
+  std::shared_ptr<LookupStreams> lookups_ = std::make_shared<LookupStreams>();
 };
 
 // ---------------------------------------------------------------------------
@@ -175,6 +180,9 @@ class GpuTable {
   void* data_ptr() const { return data_; }
 
   std::shared_mutex& uvm_mutex() { return uvm_mu_; }
+  // lookup streams of every context that reads this table (the private
+  // stream included): inserts, updates and erases order themselves after them
+  const std::shared_ptr<LookupStreams>& lookup_streams() const { return lookups_; }
 
  private:
   // runs on stream s (the modify stream or the table's private stream)
@@ -227,6 +235,7 @@ class GpuTable {
   uint64_t pipeline_task_size_ = 1024;  // PipelineGather keys per host task
   std::mutex modify_mu_;        // one modify at a time
   std::shared_mutex uvm_mu_;    // lookups shared, modifies exclusive
+  std::shared_ptr<LookupStreams> lookups_ = std::make_shared<LookupStreams>();
 };
 
 // ---------------------------------------------------------------------------
@@ -286,6 +295,7 @@ class LinearUVMEmbeddingLayer : public EmbeddingLayer {
   void erase(ExecutionContext& ctx, int64_t n, const void* keys, int64_t table_id) override;
 
   GpuTable& table() { return *table_; }
+  std::shared_ptr<LookupStreams> lookup_streams() const override { return table_->lookup_streams(); }
 
  private:
   void auto_insert(ExecutionContext& ctx, int64_t n, const void* d_keys, float hitrate);

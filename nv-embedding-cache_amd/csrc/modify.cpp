@@ -8,9 +8,10 @@
 //        -> (2) group by set: stable radix sort of (set, histogram index)
 //                (ec_set_associative_modify.cuh:364-513)
 //        -> (3) per-set replacement kernel -> records (slot, tag, source row)
-//        -> (4) invalidate the records' tags, drain the device, copy the rows,
-//                commit the tags (ec_set_associative_device_modify.cuh:225-288,
-//                :428-451)
+//        -> (4) invalidate the records' tags, order the copy after the lookups
+//                queued on the table's registered lookup streams, copy the
+//                rows, commit the tags (ec_set_associative_device_modify.cuh:
+//                225-288, :428-451)
 // The host reads three counts back (unique keys, represented sets, records),
 // where the reference also synchronizes (gather_keys_data_ptrs.cuh:168,
 // ec_set_associative_modify.cuh:489, ec_set_associative_device_modify.cuh:443).
@@ -196,10 +197,11 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
 
   // ---- (4) invalidate -> drain -> copy -> commit ----
   NVE_HIP(launch_invalidate(d_count + 1, m, rec_slot, tags_, key_bytes_, cfg_.invalid_key, s));
+  // Lookups queued from here on see the invalidated tags (the invalidation is
+  // complete before the host goes on); lookups queued earlier may still read
+  // the old rows of those ways, so the copy waits for them
   NVE_HIP(hipStreamSynchronize(s));
-  // lookups already queued on other streams may still read the old rows of
-  // the invalidated ways: let them finish before the rows are overwritten
-  NVE_HIP(hipDeviceSynchronize());
+  lookups_->order_before(s);
   uintptr_t align = (uintptr_t)rows | (uintptr_t)row_stride;
   const int src_align = (align % 16 == 0) ? 16 : (align % 4 == 0) ? 4 : 1;
   NVE_HIP(launch_copy_rows(d_count + 1, m, rec_slot, rec_src, src_align, data_,

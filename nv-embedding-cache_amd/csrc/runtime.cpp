@@ -55,6 +55,37 @@ StreamQueue::StreamQueue(hipStream_t caller, hipStream_t run)
   }
 }
 
+// ---------------------------------------------------------------------------
+void LookupStreams::add(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(mu_);
+  ++streams_[s];
+}
+
+void LookupStreams::remove(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(mu_);
+  auto it = streams_.find(s);
+  if (it != streams_.end() && --it->second == 0) streams_.erase(it);
+}
+
+void LookupStreams::order_before(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(mu_);
+  hipEvent_t e = order_event();
+  for (const auto& kv : streams_) {
+    if (kv.first == s) continue;  // in stream order already
+    NVE_HIP(hipEventRecord(e, kv.first));
+    NVE_HIP(hipStreamWaitEvent(s, e, 0));
+  }
+}
+
+void LookupStreams::drain() {
+  std::lock_guard<std::mutex> lk(mu_);
+  hipEvent_t e = order_event();
+  for (const auto& kv : streams_) {
+    NVE_HIP(hipEventRecord(e, kv.first));
+    NVE_HIP(hipEventSynchronize(e));
+  }
+}
+
 StreamQueue::~StreamQueue() {
   if (stream != caller_) {
     try {
@@ -149,11 +180,17 @@ ExecutionContext::ExecutionContext(int device, hipStream_t lookup, hipStream_t m
   if (!pool_) pool_ = ThreadPool::default_pool();
 }
 
+void ExecutionContext::watch(const std::shared_ptr<LookupStreams>& streams) {
+  streams->add(lookup_);
+  watched_.push_back(streams);
+}
+
 ExecutionContext::~ExecutionContext() {
   try {
     wait();
   } catch (...) {
   }
+  for (auto& w : watched_) w->remove(lookup_);
   for (auto& kv : bufs_)
     if (kv.second.plain) std::free(kv.second.ptr);
   if (device_ < 0 && misses_ == nullptr) return;  // a host context holds no HIP memory

@@ -93,6 +93,28 @@ class StreamQueue {
   const hipStream_t caller_;
 };
 
+// The lookup streams of the execution contexts that read one table (a
+// ContextRegistry, layer_utils.hpp:66-82).  A modify that must not overwrite
+// rows a queued lookup may still read orders itself after every lookup queued
+// so far, on the device or on the host, instead of draining the whole device
+// (ec_set_associative_device_modify.cuh:428-446): streams of other work, a
+// model's compute streams for one, are left alone.  A stream is counted once
+// per context that registered it.
+class LookupStreams {
+ public:
+  void add(hipStream_t s);
+  void remove(hipStream_t s);
+  // Work queued on `s` after this call starts after every lookup queued so
+  // far on the registered streams (one event record and stream wait each).
+  void order_before(hipStream_t s);
+  // Returns when every lookup queued so far on the registered streams is done.
+  void drain();
+
+ private:
+  std::mutex mu_;
+  std::map<hipStream_t, int> streams_;
+};
+
 // ---------------------------------------------------------------------------
 // thread pool (SimpleThreadPool: default workers = max(cores - 2, 1))
 // ---------------------------------------------------------------------------
@@ -143,6 +165,10 @@ class ExecutionContext {
   // Lookup counter of a host table (LinearHostTable counts resolved keys).
   int64_t& host_lookup_counter() { return host_counter_; }
 
+  // Register this context's lookup stream with the table that `streams`
+  // belongs to, until the context is destroyed.
+  void watch(const std::shared_ptr<LookupStreams>& streams);
+
   // Device counter of cache misses (zeroed by reset_misses on lookup_stream).
   unsigned long long* miss_counter();
   void reset_misses();
@@ -167,6 +193,7 @@ class ExecutionContext {
   int64_t host_counter_ = 0;
   std::mutex pending_mu_;
   std::vector<std::future<void>> pending_;
+  std::vector<std::shared_ptr<LookupStreams>> watched_;
 };
 
 // ---------------------------------------------------------------------------

@@ -108,7 +108,7 @@ void GpuTable::modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, cons
     NVE_HIP(launch_invalidate(num, m, slot, tags_, key_bytes_, cfg_.invalid_key, s));
     // lookups queued before the invalidation may still read these rows
     NVE_HIP(hipStreamSynchronize(s));
-    NVE_HIP(hipDeviceSynchronize());
+    lookups_->order_before(s);
     if (accumulate)
       NVE_HIP(launch_accumulate_rows(num, m, slot, src, data_, (uint64_t)cfg_.row_size_in_bytes,
                                      dtype, s));
@@ -136,7 +136,7 @@ void GpuTable::update(ExecutionContext& ctx, int64_t n, const void* keys, int64_
       ctx, "update_values", values, (size_t)(n - 1) * value_stride + value_size, s));
   if (cfg_.uvm_table != nullptr && !cfg_.disable_uvm_update) {
     std::unique_lock<std::shared_mutex> lk(uvm_mu_);
-    NVE_HIP(hipDeviceSynchronize());
+    lookups_->order_before(s);  // queued lookups read the old backing rows
     NVE_HIP(launch_table_update(d_keys, n, key_bytes_, d_vals, value_stride,
                                 static_cast<uint8_t*>(cfg_.uvm_table),
                                 (uint64_t)cfg_.row_size_in_bytes, (uint64_t)cfg_.uvm_num_rows, s));
@@ -162,7 +162,7 @@ void GpuTable::update_accumulate(ExecutionContext& ctx, int64_t n, const void* k
     const uint8_t* h_vals = static_cast<const uint8_t*>(host_input(
         ctx, "accumulate_values_host", values, (size_t)(n - 1) * value_stride + value_size, s));
     std::unique_lock<std::shared_mutex> lk(uvm_mu_);
-    NVE_HIP(hipDeviceSynchronize());
+    lookups_->drain();  // host threads write the rows queued lookups may read
     host_accumulate(ctx.pool(), h_keys, key_bytes_, n, h_vals, value_stride,
                     static_cast<uint8_t*>(cfg_.uvm_table), cfg_.row_size_in_bytes,
                     (uint64_t)cfg_.uvm_num_rows, update_dtype);
@@ -198,7 +198,7 @@ void GPUEmbeddingLayer::update(ExecutionContext& ctx, int64_t n, const void* key
   const uint8_t* d_vals = static_cast<const uint8_t*>(device_input(
       ctx, "update_values", values, (size_t)(n - 1) * value_stride + value_size, s));
   std::lock_guard<std::mutex> lk(launch_mu_);
-  NVE_HIP(hipDeviceSynchronize());  // lookups issued before this call read the old rows
+  lookups_->order_before(s);  // lookups issued before this call read the old rows
   NVE_HIP(launch_table_update(d_keys, n, key_bytes_, d_vals, value_stride,
                               static_cast<uint8_t*>(cfg_.embedding_table),
                               (uint64_t)cfg_.embedding_width_in_bytes,
@@ -223,7 +223,7 @@ void GPUEmbeddingLayer::accumulate(ExecutionContext& ctx, int64_t n, const void*
   const uint8_t* d_vals = static_cast<const uint8_t*>(device_input(
       ctx, "update_values", values, (size_t)(n - 1) * value_stride + value_size, s));
   std::lock_guard<std::mutex> lk(launch_mu_);
-  NVE_HIP(hipDeviceSynchronize());
+  lookups_->order_before(s);  // see update
   NVE_HIP(launch_table_accumulate(d_keys, n, key_bytes_, d_vals, value_stride,
                                   static_cast<uint8_t*>(cfg_.embedding_table),
                                   (uint64_t)cfg_.embedding_width_in_bytes,
