@@ -421,11 +421,12 @@ void update_rows(ThreadPool& tp, int64_t num_threads, int64_t n, const void* key
   });
 }
 
-void accumulate_rows_f32(ThreadPool& tp, int64_t num_threads, int64_t n, const void* keys, int key_bytes,
-                         const uint8_t* updates, int64_t update_stride, uint8_t* table,
-                         int64_t row_bytes, uint64_t num_rows) {
+void accumulate_rows(ThreadPool& tp, int64_t num_threads, int64_t n, const void* keys, int key_bytes,
+                     const uint8_t* updates, int64_t update_stride, uint8_t* table,
+                     int64_t row_bytes, uint64_t num_rows, int dtype) {
   if (n <= 0) return;
-  const int64_t count = row_bytes / 4;
+  const bool f16 = dtype == kF16;
+  const int64_t count = row_bytes / (f16 ? 2 : 4);
   const std::vector<int64_t> pos = positions_by_key(n, keys, key_bytes);
   const std::vector<int64_t> edges = run_edges(pos, keys, key_bytes, num_threads);
   run_tasks(tp, (int64_t)edges.size() - 1, [&](int64_t t) {
@@ -433,9 +434,16 @@ void accumulate_rows_f32(ThreadPool& tp, int64_t num_threads, int64_t n, const v
       const int64_t i = pos[(size_t)j];
       const int64_t k = load_key(keys, key_bytes, i);
       if (!in_range(k, num_rows)) continue;
-      float* dst = reinterpret_cast<float*>(table + (uint64_t)k * row_bytes);
+      uint8_t* dst = table + (uint64_t)k * row_bytes;
       const uint8_t* src = updates + i * update_stride;
-      for (int64_t e = 0; e < count; ++e) dst[e] = dst[e] + ld_f32(src + 4 * e);
+      if (f16) {
+        uint16_t* dh = reinterpret_cast<uint16_t*>(dst);
+        for (int64_t e = 0; e < count; ++e)
+          dh[e] = float_to_half_bits(half_bits_to_float(dh[e]) + half_bits_to_float(ld_u16(src + 2 * e)));
+      } else {
+        float* df = reinterpret_cast<float*>(dst);
+        for (int64_t e = 0; e < count; ++e) df[e] = df[e] + ld_f32(src + 4 * e);
+      }
     }
   });
 }

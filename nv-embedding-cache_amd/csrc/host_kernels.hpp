@@ -78,12 +78,13 @@ void update_rows(ThreadPool& pool, int64_t num_threads, int64_t n, const void* k
                  const uint8_t* values, int64_t value_stride, uint8_t* table, int64_t row_bytes,
                  uint64_t num_rows);
 
-// cpu_kernel_update_accumulate for f32 rows: table row keys[i] += update i.
-// Work is split by key, so every row has one writer and a repeated key's
-// updates are added in position order: the result is deterministic.
-void accumulate_rows_f32(ThreadPool& pool, int64_t num_threads, int64_t n, const void* keys,
-                         int key_bytes, const uint8_t* updates, int64_t update_stride,
-                         uint8_t* table, int64_t row_bytes, uint64_t num_rows);
+// cpu_kernel_update_accumulate: table row keys[i] += update i, rows of f32
+// (dtype kF32) or f16 (kF16: each element widened, added in f32, rounded
+// back).  Work is split by key, so every row has one writer and a repeated
+// key's updates are added in position order: the result is deterministic.
+void accumulate_rows(ThreadPool& pool, int64_t num_threads, int64_t n, const void* keys,
+                     int key_bytes, const uint8_t* updates, int64_t update_stride, uint8_t* table,
+                     int64_t row_bytes, uint64_t num_rows, int dtype);
 
 // true when the 8-wide AVX2 + F16C + FMA loops are in use on this host
 bool vector_loops();

@@ -142,10 +142,9 @@ void LinearHostTable::update_accumulate(ExecutionContext& ctx, int64_t n, const 
   NVE_CHECK(value_type == kF32, "Unsupported update type ", value_type);
   const void* hk = host_view_in(ctx, "update_keys", keys, (size_t)n * key_bytes_);
   const void* hv = host_view_in(ctx, "update_values", values, (size_t)n * value_stride);
-  hostk::accumulate_rows_f32(ctx.pool(), threads(ctx), n, hk, key_bytes_,
-                             static_cast<const uint8_t*>(hv), value_stride,
-                             static_cast<uint8_t*>(cfg_.emb_table), cfg_.row_bytes,
-                             (uint64_t)cfg_.num_rows);
+  hostk::accumulate_rows(ctx.pool(), threads(ctx), n, hk, key_bytes_, static_cast<const uint8_t*>(hv),
+                         value_stride, static_cast<uint8_t*>(cfg_.emb_table), cfg_.row_bytes,
+                         (uint64_t)cfg_.num_rows, kF32);
 }
 
 std::shared_ptr<ExecutionContext> LinearHostTable::create_execution_context(

@@ -20,6 +20,7 @@
 
 #include "kernels/cache_launch.hpp"
 #include "kernels/modify_launch.hpp"
+#include "host_kernels.hpp"
 #include "kernels/update_launch.hpp"
 #include "layers.hpp"
 
@@ -34,43 +35,14 @@ T* carve(uint8_t*& p, size_t count) {
   return r;
 }
 
-int64_t host_key(const void* keys, int key_bytes, int64_t i) {
-  return key_bytes == 4 ? (int64_t) static_cast<const int32_t*>(keys)[i]
-                        : static_cast<const int64_t*>(keys)[i];
-}
-
 // rows[key] += vals[i] on the host for keys inside [0, num_rows), in the
-// table's float type; keys are split over the pool's workers in contiguous
-// runs, so a repeated key's additions happen in one worker in key order
-// unless the repeats straddle two runs.
+// table's float type, split over the pool's workers by key: each row has one
+// writer and a repeated key's additions are made in position order.
 void host_accumulate(ThreadPool& pool, const void* keys, int key_bytes, int64_t n,
                      const uint8_t* vals, int64_t stride, uint8_t* rows, int64_t row_bytes,
                      uint64_t num_rows, int dtype) {
-  const int64_t workers = std::max<int64_t>(1, pool.num_workers());
-  const int64_t per = std::max<int64_t>(512, (n + workers - 1) / workers);
-  std::vector<std::future<void>> fs;
-  for (int64_t b = 0; b < n; b += per) {
-    const int64_t e = std::min(n, b + per);
-    fs.push_back(pool.submit([=] {
-      for (int64_t i = b; i < e; ++i) {
-        const uint64_t key = (uint64_t)host_key(keys, key_bytes, i);
-        if (key >= num_rows) continue;  // outside the table (negative keys wrap above it)
-        uint8_t* d = rows + key * (uint64_t)row_bytes;
-        const uint8_t* s = vals + i * stride;
-        if (dtype == kF32) {
-          float* df = reinterpret_cast<float*>(d);
-          const float* sf = reinterpret_cast<const float*>(s);
-          for (int64_t j = 0; j < row_bytes / 4; ++j) df[j] += sf[j];
-        } else {
-          uint16_t* dh = reinterpret_cast<uint16_t*>(d);
-          const uint16_t* sh = reinterpret_cast<const uint16_t*>(s);
-          for (int64_t j = 0; j < row_bytes / 2; ++j)
-            dh[j] = float_to_half_bits(half_bits_to_float(dh[j]) + half_bits_to_float(sh[j]));
-        }
-      }
-    }));
-  }
-  for (auto& f : fs) f.get();
+  hostk::accumulate_rows(pool, pool.num_workers(), n, keys, key_bytes, vals, stride, rows, row_bytes,
+                         num_rows, dtype);
 }
 
 void check_update_args(int64_t n, const void* keys, const void* values, int64_t stride,

@@ -172,6 +172,32 @@ def test_accumulate_contended_fp16_row():
     ct.close()
 
 
+@pytest.mark.parametrize("dtype", [O.F32, O.F16])
+def test_backing_accumulate_of_spread_repeats_is_in_position_order(dtype):
+    """Repeated keys spread over 6000 positions (far beyond one worker's share
+    of the batch): every backing row gets its updates one at a time, in
+    position order -- bit for bit the sequential sum, on values whose sums
+    round (not dyadic), so a lost add or another order shows."""
+    rng = np.random.default_rng(60 + dtype)
+    rows, dim, n = 50, 24, 6000
+    npd = np.float32 if dtype == O.F32 else np.float16
+    base = rng.normal(0, 1, size=(rows, dim)).astype(npd)
+    uvm = base.view(np.uint8).reshape(rows, -1)
+    ct = CachedTable(uvm, 64 * 1024, 8, value_dtype=_lib.DT_F32 if dtype == O.F32 else _lib.DT_F16)
+    keys = rng.integers(0, rows, size=n).astype(np.int64)
+    upd = rng.normal(0, 1, size=(n, dim)).astype(npd)
+    d_keys, d_upd = to_dev(keys), to_dev(upd.view(np.uint8).reshape(-1))
+    _lib.call("nve_table_update_accumulate", ct.table, ct.ctx, n, vp(d_keys), dim * upd.itemsize,
+              dim * upd.itemsize, vp(d_upd), _lib.DT_F32 if dtype == O.F32 else _lib.DT_F16)
+    torch.cuda.synchronize()
+    want = base.copy()
+    for i in range(n):  # fp32 add per element, rounded back to the row type
+        want[keys[i]] = (want[keys[i]].astype(np.float32) + upd[i].astype(np.float32)).astype(npd)
+    got = table_host(ct).view(npd).reshape(rows, dim)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+    ct.close()
+
+
 def test_accumulate_rejects_other_value_types():
     rows, dim = 100, 8
     ct = CachedTable(np.zeros((rows, dim * 4), np.uint8), 64 * 1024, 8)
