@@ -176,6 +176,16 @@ NVE_C_API nve_status_t nve_amd_pooling_backprop(
     nve_data_type_t grad_type, int64_t embedding_width, void* unique_keys_out, void* grads_out,
     int64_t* num_unique_out, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Log level (include/logging.hpp:34-203): messages at or below the level are
+ * written, errors to stderr and the rest to stdout.  Levels: 0 critical,
+ * 10 error, 20 warning, 30 perf, 40 info, 100 verbose.  The initial level is
+ * NVE_LOG_LEVEL's (CRITICAL, ERROR, WARNING, PERF, INFO or VERBOSE), else
+ * warning.  Library calls are also marked as roctx ranges (rocprofv3
+ * --marker-trace) unless NVE_ROCTX=0; the reference marks them with NVTX
+ * (include/cuda_support.hpp:26-55). */
+NVE_C_API nve_status_t nve_amd_set_log_level(int32_t level);
+NVE_C_API nve_status_t nve_amd_get_log_level(int32_t* level);
+
 #ifdef __cplusplus
 }
 #endif

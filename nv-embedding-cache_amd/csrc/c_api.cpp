@@ -14,6 +14,7 @@
 #include "host_layer.hpp"
 #include "kernels/noalloc_launch.hpp"
 #include "layers.hpp"
+#include "trace.hpp"
 
 using namespace nve_amd;
 
@@ -47,6 +48,9 @@ thread_local std::string g_last_error;
 
 nve_status_t set_error(nve_status_t s, const std::string& m) {
   g_last_error = m;
+  // rejected arguments and unsupported features are the caller's to handle
+  const bool expected = s == NVE_ERROR_INVALID_ARGUMENT || s == NVE_ERROR_NOT_IMPLEMENTED;
+  log_at(expected ? LogLevel::Info : LogLevel::Error, "status ", (int)s, ": ", m);
   return s;
 }
 
@@ -330,6 +334,7 @@ nve_status_t nve_table_find(nve_table_t table, nve_context_t ctx, int64_t n, con
                             int64_t* value_sizes) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_find");
   if (table->host)
     table->host->find_any(*ctx->ptr, n, keys, hit_mask, value_stride, values, value_sizes);
   else
@@ -342,6 +347,7 @@ nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, c
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_insert");
   if (table->host) return NVE_SUCCESS;  // a linear host table holds every row: no effect
   table->ptr->insert(*ctx->ptr, n, keys, value_stride, value_size, values);
   return NVE_SUCCESS;
@@ -352,6 +358,7 @@ nve_status_t nve_table_update(nve_table_t table, nve_context_t ctx, int64_t n, c
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_update");
   if (table->host)
     table->host->update(*ctx->ptr, n, keys, value_stride, value_size, values);
   else
@@ -366,6 +373,7 @@ nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, i
                                          nve_data_type_t value_type) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_update_accumulate");
   if (table->host)
     table->host->update_accumulate(*ctx->ptr, n, keys, value_stride, value_size, values,
                                    dtype_in(value_type));
@@ -379,6 +387,7 @@ nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, i
 nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_clear");
   if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
   table->ptr->clear(*ctx->ptr);
   return NVE_SUCCESS;
@@ -388,6 +397,7 @@ nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
 nve_status_t nve_table_erase(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys) {
   NEED_TABLE_CTX
   C_TRY
+  NVE_TRACE("nve_table_erase");
   if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
   table->ptr->erase(*ctx->ptr, n, keys);
   return NVE_SUCCESS;
@@ -574,6 +584,7 @@ nve_status_t nve_layer_lookup(nve_layer_t layer, nve_context_t ctx, int64_t num_
                               uint64_t* hitmask, float* hitrates) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_lookup");
   layer->ptr->lookup(*ctx->ptr, num_keys, keys, output, output_stride, hitmask, nullptr, hitrates);
   return NVE_SUCCESS;
   C_CATCH
@@ -588,6 +599,7 @@ nve_status_t nve_layer_lookup_pooled(nve_layer_t layer, nve_context_t ctx, int64
                                      nve_data_type_t output_type, float* hitrates) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_lookup_pooled");
   const int out_t = dtype_in(output_type);
   if (out_t == kUnknown)
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "output_type must be a supported, non-UNKNOWN data type");
@@ -612,6 +624,7 @@ nve_status_t nve_layer_insert(nve_layer_t layer, nve_context_t ctx, int64_t num_
                               const void* values, int64_t table_id) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_insert");
   layer->ptr->insert(*ctx->ptr, num_keys, keys, value_stride, value_size, values, table_id);
   return NVE_SUCCESS;
   C_CATCH
@@ -622,6 +635,7 @@ nve_status_t nve_layer_update(nve_layer_t layer, nve_context_t ctx, int64_t num_
                               const void* values, int64_t table_id) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_update");
   layer->ptr->update(*ctx->ptr, num_keys, keys, value_stride, value_size, values, table_id);
   return NVE_SUCCESS;
   C_CATCH
@@ -633,6 +647,7 @@ nve_status_t nve_layer_accumulate(nve_layer_t layer, nve_context_t ctx, int64_t 
                                   int64_t table_id) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_accumulate");
   layer->ptr->accumulate(*ctx->ptr, num_keys, keys, value_stride, value_size, values,
                          dtype_in(value_type), table_id);
   return NVE_SUCCESS;
@@ -642,6 +657,7 @@ nve_status_t nve_layer_accumulate(nve_layer_t layer, nve_context_t ctx, int64_t 
 nve_status_t nve_layer_clear(nve_layer_t layer, nve_context_t ctx) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_clear");
   layer->ptr->clear(*ctx->ptr);
   return NVE_SUCCESS;
   C_CATCH
@@ -651,6 +667,7 @@ nve_status_t nve_layer_erase(nve_layer_t layer, nve_context_t ctx, int64_t num_k
                              const void* keys, int64_t table_id) {
   NEED_LAYER_CTX
   C_TRY
+  NVE_TRACE("nve_layer_erase");
   layer->ptr->erase(*ctx->ptr, num_keys, keys, table_id);
   return NVE_SUCCESS;
   C_CATCH
@@ -694,6 +711,7 @@ nve_status_t nve_amd_find_and_pool(nve_key_type_t key_type, int64_t num_keys, co
                                    int64_t output_stride, int32_t split_hint,
                                    int32_t unroll_hint, void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_find_and_pool");
   const int kb = key_bytes_of(key_type);
   const int vdt = dtype_in(value_dtype);
   const int odt = dtype_in(output_type);
@@ -785,6 +803,7 @@ nve_status_t nve_amd_find_and_pool_multi(nve_key_type_t key_type, int64_t num_ta
                                          nve_pooling_type_t pooling_type,
                                          nve_data_type_t output_type, void* output, void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_find_and_pool_multi");
   const int kb = key_bytes_of(key_type);
   const int vdt = dtype_in(value_dtype);
   const int odt = dtype_in(output_type);
@@ -859,6 +878,7 @@ nve_status_t nve_amd_dedup(nve_key_type_t key_type, int64_t num_keys, const void
                            int64_t* num_unique, void* workspace, uint64_t workspace_bytes,
                            void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_dedup");
   NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
   NVE_CHECK_ARG(num_unique != nullptr, "num_unique must not be NULL");
   if (num_keys > 0)
@@ -889,6 +909,7 @@ nve_status_t nve_amd_pooling_backprop(nve_key_type_t key_type, int64_t num_keys,
                                       void* unique_keys_out, void* grads_out, int64_t* num_unique_out,
                                       void* workspace, uint64_t workspace_bytes, void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_pooling_backprop");
   NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
   NVE_CHECK_ARG(num_unique_out != nullptr, "num_unique_out must not be NULL");
   const bool concat = pooling_type == NVE_POOL_CONCATENATE;
@@ -917,6 +938,7 @@ nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num_keys, con
                                   void* output, int64_t output_stride, void* workspace,
                                   uint64_t workspace_bytes, void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_dedup_gather");
   NVE_CHECK_ARG(num_keys >= 0, "Invalid num_keys");
   NVE_CHECK_ARG(num_rows > 0 && row_size_in_bytes > 0, "Invalid table shape");
   NVE_CHECK_ARG(output_stride >= row_size_in_bytes, "output_stride is smaller than a row");
@@ -932,6 +954,7 @@ nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_k
                                           const void* table, int64_t num_rows, int64_t row_size_in_bytes,
                                           void* output, int64_t output_stride, void* stream) {
   C_TRY
+  NVE_TRACE("nve_amd_dedup_gather_noalloc");
   NVE_CHECK_ARG(num_keys >= 0 && num_keys <= kNoAllocMaxKeys, "num_keys must be in [0, ", kNoAllocMaxKeys,
                 "] for the allocation-free dedup gather (got ", num_keys, ")");
   NVE_CHECK_ARG(num_rows > 0 && row_size_in_bytes > 0, "Invalid table shape");
@@ -947,6 +970,18 @@ nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_k
                    row_size_in_bytes, output, output_stride, ws, need, (hipStream_t)stream);
   return NVE_SUCCESS;
   C_CATCH
+}
+
+nve_status_t nve_amd_set_log_level(int32_t level) {
+  if (level < 0) return set_error(NVE_ERROR_INVALID_ARGUMENT, "log level must not be negative");
+  set_log_level(level);
+  return NVE_SUCCESS;
+}
+
+nve_status_t nve_amd_get_log_level(int32_t* level) {
+  if (!level) return set_error(NVE_ERROR_INVALID_ARGUMENT, "level must not be NULL");
+  *level = log_level();
+  return NVE_SUCCESS;
 }
 
 nve_status_t nve_amd_read_ceiling(const void* table, int64_t row_size_in_bytes, const int64_t* idx,
@@ -992,6 +1027,7 @@ nve_status_t nve_amd_table_insert_from_uvm(nve_table_t table, nve_context_t ctx,
   NEED_TABLE_CTX
   if (!table->ptr) return set_error(NVE_ERROR_INVALID_ARGUMENT, "table must be a GPU table");
   C_TRY
+  NVE_TRACE("nve_amd_table_insert_from_uvm");
   table->ptr->insert_from_uvm(*ctx->ptr, n, keys);
   return NVE_SUCCESS;
   C_CATCH

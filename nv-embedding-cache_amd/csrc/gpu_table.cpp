@@ -16,6 +16,7 @@
 
 #include "kernels/cache_launch.hpp"
 #include "layers.hpp"
+#include "trace.hpp"
 
 namespace nve_amd {
 
@@ -48,6 +49,10 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   NVE_CHECK(num_sets_ <= UINT32_MAX, "Too many cache sets");
   const uint64_t ways = num_sets_ * kWays;
   const size_t data_bytes = (size_t)ways * (size_t)cfg_.row_size_in_bytes;
+  NVE_LOG_INFO("GpuTable on device ", cfg_.device_id, ": ", num_sets_, " sets of 8 ways, ",
+               data_bytes, " bytes of rows in ", cfg_.data_storage_on_host ? "host" : "device",
+               " memory, ", cfg_.uvm_table ? "with" : "without", " a backing table, ",
+               cfg_.modify_on_gpu ? "device" : "host", " replacement policy");
   if (cfg_.data_storage_on_host)
     NVE_HIP(hipHostMalloc((void**)&data_, data_bytes, hipHostMallocDefault));
   else

@@ -11,6 +11,7 @@
 #include <cstring>
 
 #include "layers.hpp"
+#include "trace.hpp"
 
 namespace nve_amd {
 
@@ -160,6 +161,7 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
   std::shared_ptr<GpuTable> table = table_;
   std::shared_ptr<std::atomic<bool>> flag = in_flight_;
   ExecutionContext* c = &ctx;
+  NVE_LOG_PERF("auto-insert of ", nk, " keys launched (hit rate ", hitrate, ")");
   ctx.add_pending(ctx.pool().submit([table, c, nk, flag, keys = std::move(keys)]() {
     struct Done {
       std::atomic<bool>* f;
