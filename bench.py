@@ -446,7 +446,7 @@ def run_workload(args, torch, _lib):
         # host table and are inserted when the heuristic asks for it
         rows, dim, alpha = args.c3_rows, 128, 1.2
         hot = args.c3_hotness
-        bags = 262144 // hot
+        bags = args.c3_keys // hot
         nkeys = bags * hot
         width = dim * 2
         log(f"c3: pinned host table {rows} x {width} B ({rows * width / 1e9:.1f} GB)")
@@ -469,6 +469,28 @@ def run_workload(args, torch, _lib):
             assert hip.hipMemcpy(host_ptr.value + r0 * width, tmp.data_ptr(), (r1 - r0) * width, 2) == 0
         del tmp
         torch.cuda.synchronize()
+        if not args.c3_no_touch:
+            import numpy as np
+            # The table was filled by DMA, so the host has never mapped its pages: the
+            # first host read of each page faults (about 11 ms per 1024-row PipelineGather
+            # task on this box).  Read one byte per 4 KiB page from host threads first, as
+            # a table loaded through host memory would already be.
+            t0 = time.perf_counter()
+            total = rows * width
+            nthreads = max(1, min(16, cpu_info()[1]))
+            span = (total + nthreads - 1) // nthreads
+
+            def touch(k):
+                b0, b1 = k * span, min(total, (k + 1) * span)
+                if b1 <= b0:
+                    return 0
+                view = np.ctypeslib.as_array((ctypes.c_uint8 * (b1 - b0)).from_address(host_ptr.value + b0))
+                return int(view[::4096].sum())  # numpy reductions run without the GIL
+
+            import concurrent.futures as cf
+            with cf.ThreadPoolExecutor(nthreads) as ex:
+                list(ex.map(touch, range(nthreads)))
+            log(f"c3: host pages touched from {nthreads} threads in {time.perf_counter() - t0:.1f} s")
         class _Host:  # the table's address, as the layer config wants it
             def data_ptr(self):
                 return host_ptr.value
@@ -553,6 +575,7 @@ def run_workload(args, torch, _lib):
                         "host_link_bytes_per_step": int(nkeys * (1 - hit)) * width,
                         "lookup": "concat" if concat else f"pooled {bags} x {hot} Sum",
                         "kernel_mode": args.kernel_mode, "prefilled": bool(args.c3_prefill),
+                        "host_pages_touched": not args.c3_no_touch,
                         "step": "lookup + hit-rate readback + auto-insert when the heuristic fires"})
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
@@ -706,6 +729,10 @@ def main():
     ap.add_argument("--c3-concat", action="store_true", help="c3: one row per key instead of pooled bags")
     ap.add_argument("--c3-hotness", type=int, default=1024, choices=[16, 32, 64, 128, 256, 512, 1024],
                     help="c3: keys per pooled bag (262,144 keys per batch in 262,144 / hotness bags)")
+    ap.add_argument("--c3-keys", type=int, default=262144,
+                    help="c3: keys per batch (a multiple of --c3-hotness)")
+    ap.add_argument("--c3-no-touch", action="store_true",
+                    help="c3: leave the DMA-filled host table's pages unmapped on the host")
     ap.add_argument("--c3-prefill", action="store_true",
                     help="c3: insert every backing row into the cache before the lookups (hit path only)")
     ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],
