@@ -79,9 +79,11 @@ NVE_C_API nve_status_t nve_amd_dedup(nve_key_type_t key_type, int64_t num_keys, 
                                      uint64_t workspace_bytes, void* stream);
 
 /* Dedup-then-gather over a linear table in device memory: output row i =
- * table row keys[i], the keys read in sorted order so each distinct row is
- * fetched once per run.  Keys outside [0, num_rows) leave their output row
- * unchanged.  Asynchronous; workspace as for nve_amd_dedup. */
+ * table row keys[i].  The keys are deduplicated by hashing, each distinct row
+ * is read from the table once into the output row of one of its positions,
+ * and the other positions copy that row (UnpackDedup).  Keys outside
+ * [0, num_rows) leave their output row unchanged.  Asynchronous; workspace as
+ * for nve_amd_dedup. */
 NVE_C_API nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num_keys,
                                             const void* keys, const void* table, int64_t num_rows,
                                             int64_t row_size_in_bytes, void* output,

@@ -1,6 +1,7 @@
 // dedup.cpp -- host orchestration of key dedup (Deduper::dedup,
-// deduper.cuh:136-221) and of the dedup-ordered gather (dedup, then one table
-// read per distinct key run, UnpackDedup, cuda_utils.cuh:24-79, fused into it).
+// deduper.cuh:136-221) and of the dedup-then-gather (a hash dedup, one table
+// read per distinct key, then UnpackDedup, cuda_utils.cuh:24-79; batches past
+// 2^30 keys sort instead and gather in key order).
 #include "dedup.hpp"
 
 #include "kernels/cache_launch.hpp"
@@ -55,9 +56,20 @@ DedupBufs carve(void* ws, int64_t n) {
 
 }  // namespace
 
+// Scratch of the hash dedup-then-gather: table keys, owners, slot per key.
+size_t hash_gather_bytes(int64_t n) {
+  const size_t slots = hash_dedup_slots(n);
+  return pad(8 * slots) + pad(4 * slots) + pad(4 * (size_t)n) + pad(8 * (size_t)n) + 256;
+}
+
+// Batches up to this size take the hash path (slot numbers fit 32 bits).
+constexpr int64_t kHashGatherMaxKeys = int64_t(1) << 30;
+
 size_t dedup_workspace_bytes(int64_t n) {
   if (n < 1) n = 1;
-  return 512 + 2 * pad(8 * n) + 4 * pad(4 * n) + pad(4 * (n + 1)) + radix_sort_temp_bytes(n);
+  const size_t sort = 512 + 2 * pad(8 * n) + 4 * pad(4 * n) + pad(4 * (n + 1)) + radix_sort_temp_bytes(n);
+  const size_t hash = n <= kHashGatherMaxKeys ? hash_gather_bytes(n) : 0;
+  return sort > hash ? sort : hash;
 }
 
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
@@ -96,6 +108,23 @@ void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t*
   if (n <= 0) return;
   NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
   NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
+  if (n <= kHashGatherMaxKeys) {
+    // hash dedup: no order is needed, only one read of each distinct row
+    uint8_t* p = static_cast<uint8_t*>(ws);
+    const size_t slots = hash_dedup_slots(n);
+    void* tab = p;  // keys of 4 or 8 bytes (room for 8)
+    p += pad(8 * slots);
+    uint32_t* owner = reinterpret_cast<uint32_t*>(p);
+    p += pad(4 * slots);
+    uint32_t* slot_of = reinterpret_cast<uint32_t*>(p);
+    p += pad(4 * (size_t)n);
+    uint64_t* owners = reinterpret_cast<uint64_t*>(p);
+    p += pad(8 * (size_t)n);
+    uint32_t* count = reinterpret_cast<uint32_t*>(p);
+    NVE_HIP(launch_hash_dedup_gather(keys, key_bytes, n, table, num_rows, row_bytes, out, out_stride, tab,
+                                     owner, slot_of, owners, count, s));
+    return;
+  }
   DedupBufs b = carve(ws, n);
   // rows of [0, num_rows): sort on the row-index bits only (keys outside the
   // table stay unresolved and their output rows untouched)

@@ -20,8 +20,8 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
                   void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
                   uint32_t* pos_key = nullptr, const uint32_t** count_dev = nullptr);
 
-// out[i] = table row keys[i] for keys in [0, num_rows), gathered in key order
-// so that repeated keys read their row back to back (asynchronous).
+// out[i] = table row keys[i] for keys in [0, num_rows), each distinct row read
+// from the table once (asynchronous).
 void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t* table,
                       int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride, void* ws,
                       size_t ws_bytes, hipStream_t s);

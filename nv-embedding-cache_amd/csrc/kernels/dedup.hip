@@ -1,11 +1,19 @@
 // dedup.hip -- key deduplication on the GPU (Deduper::dedup, deduper.cuh:136-221)
-// and the dedup-ordered gather.
+// and the dedup-then-gather.
 //
 // dedup: stable radix sort of (key, position) -> run heads -> exclusive scan
 // -> per run: unique key, start offset; per position: inverse = original
 // position in key order; counts from consecutive starts.  Outputs match the
 // reference's: unique keys ascending (signed order), counts, the stable
 // inverse map and exclusive offsets.
+//
+// dedup-then-gather needs no order, so it dedups by hashing instead of
+// sorting (four launches instead of eleven): every distinct key of a
+// workgroup claims a slot of an open-addressed table (linear probing, at most
+// half full) with one compare-and-swap, the winner becoming the key's owner;
+// the owners copy their row from the table (each distinct row read once),
+// then every other position copies its owner's output row (UnpackDedup,
+// cuda_utils.cuh:24-79).
 #include "device_common.cuh"
 #include "dedup_launch.hpp"
 
@@ -50,6 +58,284 @@ __global__ __launch_bounds__(256) void dedup_counts_kernel(const uint32_t* start
   const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t m = u_dev != nullptr ? *u_dev : u_n;
   if (u < m) store_key(counts, key_bytes, u, (int64_t)(start[u + 1] - start[u]));
+}
+
+// ---------------------------------------------------------------------------
+// hash dedup for the gather
+// ---------------------------------------------------------------------------
+constexpr uint32_t kNoSlot = 0xffffffffu;
+
+// Table keys are 32-bit when every row index fits (num_rows < 2^32), else
+// 64-bit; all ones marks an empty slot (no row index has that value).
+template <typename KT>
+constexpr KT empty_slot() {
+  return (KT)~(KT)0;
+}
+
+// the table's keys to empty, and the owner count to 0
+template <typename KT>
+__global__ __launch_bounds__(256) void hash_clear_kernel(KT* tab, int64_t slots, uint32_t* count) {
+  constexpr int64_t per = 16 / sizeof(KT);  // slots per 16-byte store
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) *count = 0;
+  if ((i + 1) * per <= slots) {
+    u32x4 e{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    reinterpret_cast<u32x4*>(tab)[i] = e;
+  } else {
+    for (int64_t j = i * per; j < slots; ++j) tab[j] = empty_slot<KT>();
+  }
+}
+
+// Multiplicative (Fibonacci) hash to `bits` bits.
+__device__ __forceinline__ uint32_t slot_hash(uint64_t k, int bits) {
+  return (uint32_t)((k * 0x9E3779B97F4A7C15ull) >> (64 - bits));
+}
+
+__device__ __forceinline__ uint32_t cas(uint32_t* p, uint32_t expect, uint32_t v) {
+  return atomicCAS(p, expect, v);
+}
+__device__ __forceinline__ uint64_t cas(uint64_t* p, uint64_t expect, uint64_t v) {
+  return (uint64_t)atomicCAS(reinterpret_cast<unsigned long long*>(p), (unsigned long long)expect,
+                             (unsigned long long)v);
+}
+
+// Claim key k's slot of a table of 2^bits slots (linear probing; the caller
+// guarantees a free slot).  Returns the slot; *won: this call put k there.
+// A slot only changes from empty to a key, so the compare-and-swap's answer
+// is final.
+template <typename KT>
+__device__ __forceinline__ uint32_t claim(KT* tab, KT k, int bits, bool* won) {
+  const uint32_t mask = (1u << bits) - 1u;
+  uint32_t h = slot_hash(k, bits);
+  for (;;) {
+    const KT cur = cas(tab + h, empty_slot<KT>(), k);
+    if (cur == empty_slot<KT>() || cur == k) {
+      *won = cur == empty_slot<KT>();
+      return h;
+    }
+    h = (h + 1) & mask;
+  }
+}
+
+constexpr int kInsertThreads = 1024;  // one key per thread
+constexpr int kLocalBits = 11;        // 2048 LDS slots per workgroup, at most half full
+
+// An owner's entry of the compact list: with 32-bit keys the key and the
+// position packed (so the copy needs no further load), else the position.
+template <typename KT>
+__device__ __forceinline__ uint64_t owner_entry(KT k, uint32_t pos) {
+  return sizeof(KT) == 4 ? ((uint64_t)k << 32) | pos : (uint64_t)pos;
+}
+
+// Each workgroup first dedups its 1024 keys in an LDS table, so a key claims
+// its global slot once per workgroup rather than once per occurrence:
+// thousands of device-scope compare-and-swaps on one hot key's slot would
+// serialize at the memory side.  The global winner of a slot owns the key:
+// it records itself in owner[slot] and in the compact owner list (one
+// atomic add per workgroup for the list's positions; per-workgroup segments
+// of the list, which need none, made the owners' copy slower: 12.1 -> 17.4 us
+// on 262,144 Zipf keys).
+template <typename KT>
+__global__ __launch_bounds__(kInsertThreads) void hash_insert_kernel(const void* keys, int key_bytes,
+                                                                     int64_t n, uint64_t num_rows, KT* tab,
+                                                                     uint32_t* owner, int bits,
+                                                                     uint32_t* slot_of, uint64_t* owners,
+                                                                     uint32_t* count) {
+  __shared__ KT lkey[1 << kLocalBits];
+  __shared__ uint32_t lslot[1 << kLocalBits];  // global slot of the local entry
+  __shared__ uint32_t wave_owners[kInsertThreads / 64];
+  __shared__ uint32_t list_base;
+  const int tid = threadIdx.x;
+  for (int j = tid; j < (1 << kLocalBits); j += kInsertThreads) lkey[j] = empty_slot<KT>();
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kInsertThreads + tid;
+  bool in = false;
+  KT k = 0;
+  if (i < n) {
+    const uint64_t k64 = (uint64_t)load_key(keys, key_bytes, i);
+    in = k64 < num_rows;  // keys outside the table get no slot and no output row
+    k = (KT)k64;
+  }
+  uint32_t ls = 0;
+  bool local_first = false;
+  if (in) ls = claim<KT>(lkey, k, kLocalBits, &local_first);
+  __syncthreads();
+  bool global_owner = false;
+  if (local_first) {
+    const uint32_t gs = claim<KT>(tab, k, bits, &global_owner);
+    lslot[ls] = gs;
+    if (global_owner) owner[gs] = (uint32_t)i;
+  }
+  // compact owner list: ranks inside the wave, wave totals, one atomic per workgroup
+  const uint64_t ballot = __ballot(global_owner);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t below = (uint32_t)__popcll(ballot & (lane == 0 ? 0ull : (~0ull >> (64 - lane))));
+  if (lane == 0) wave_owners[wave] = (uint32_t)__popcll(ballot);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t total = 0;
+    for (int w = 0; w < kInsertThreads / 64; ++w) {
+      const uint32_t c = wave_owners[w];
+      wave_owners[w] = total;
+      total += c;
+    }
+    list_base = total ? atomicAdd(count, total) : 0u;
+  }
+  __syncthreads();
+  if (global_owner) owners[list_base + wave_owners[wave] + below] = owner_entry<KT>(k, (uint32_t)i);
+  if (i < n) slot_of[i] = in ? lslot[ls] : kNoSlot;
+}
+
+// PASS 0: the owners (owners[0 .. *count)) copy their key's table row to
+// their output row; PASS 1: every other position copies its owner's output
+// row.  A wave resolves T positions (one per lane), then groups of G lanes
+// move one row each, U rows in flight, VB bytes per lane and load.
+struct HashCopy {
+  const void* keys;
+  int key_bytes;
+  int64_t n;
+  const uint8_t* table;
+  uint64_t row_bytes;
+  const uint32_t* slot_of;
+  const uint32_t* owner;
+  const uint64_t* owners;
+  const uint32_t* count;
+  uint8_t* out;
+  int64_t out_stride;
+};
+
+template <int VB, int U, int PASS, bool PACKED>
+__global__ __launch_bounds__(256) void hash_copy_kernel(HashCopy a, int g_shift, int t_shift,
+                                                        int passes) {
+  const int T = 1 << t_shift;
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t base = tile << t_shift;
+  const int64_t limit = PASS == 0 ? (int64_t)*a.count : a.n;
+  if (base >= limit) return;  // whole wave past the end
+  const int64_t j = base + lane;
+  uint64_t src = 0;   // row to copy from, 0: nothing to do for this lane's position
+  uint32_t dst = 0;   // output row
+  if (lane < T && j < limit) {
+    if (PASS == 0) {
+      const uint64_t e = a.owners[j];
+      dst = (uint32_t)e;
+      const uint64_t key = PACKED ? e >> 32 : (uint64_t)load_key(a.keys, a.key_bytes, dst);
+      src = (uint64_t)a.table + key * a.row_bytes;
+    } else {
+      dst = (uint32_t)j;
+      const uint32_t sl = a.slot_of[j];
+      if (sl != kNoSlot) {
+        const uint32_t own = a.owner[sl];
+        if (own != (uint32_t)j) src = (uint64_t)a.out + (uint64_t)own * (uint64_t)a.out_stride;
+      }
+    }
+  }
+  const int G = 1 << g_shift;
+  const int gl = lane & (G - 1);
+  const int grp = lane >> g_shift;
+  const int groups = 64 >> g_shift;
+  const int per_group = T >> (6 - g_shift) > 0 ? T >> (6 - g_shift) : 1;
+  const uint64_t zero_row = (uint64_t)g_zero_row;
+  for (int p = 0; p < passes; ++p) {
+    const int64_t off = ((int64_t)p * G + gl) * VB;
+    const bool in_row = off < (int64_t)a.row_bytes;
+    for (int q0 = 0; q0 < per_group; q0 += U) {
+      uint64_t ra[U];
+      uint32_t rd[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = q0 + u;
+        const int from = grp + (q < per_group ? q : 0) * groups;
+        ra[u] = shfl64(src, from);
+        rd[u] = shfl32(dst, from);
+        if (q >= per_group) ra[u] = 0;
+      }
+      Vec<VB> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool real = ra[u] != 0;
+        v[u] = load_vec<VB>((real ? ra[u] : zero_row) + ((real && in_row) ? off : (off & kZeroRowMask)));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (ra[u] == 0 || !in_row) continue;
+        store_vec<VB>(a.out + (int64_t)rd[u] * a.out_stride + off, v[u]);
+      }
+    }
+  }
+}
+
+size_t hash_dedup_slots(int64_t n) {
+  size_t s = 1024;
+  while (s < 2 * (size_t)n) s <<= 1;
+  return s;
+}
+
+size_t hash_dedup_key_bytes(int64_t num_rows) { return (uint64_t)num_rows <= 0xffffffffull ? 4 : 8; }
+
+hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, const uint8_t* table,
+                                    int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride,
+                                    void* tab, uint32_t* owner, uint32_t* slot_of, uint64_t* owners,
+                                    uint32_t* count, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t slots = (int64_t)hash_dedup_slots(n);
+  int bits = 0;
+  while ((1ll << bits) < slots) ++bits;
+  const bool k32 = hash_dedup_key_bytes(num_rows) == 4;
+  if (k32) {
+    hipLaunchKernelGGL(hash_clear_kernel<uint32_t>, dim3((slots / 4 + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(tab), slots, count);
+    hipLaunchKernelGGL(hash_insert_kernel<uint32_t>, dim3((n + kInsertThreads - 1) / kInsertThreads),
+                       dim3(kInsertThreads), 0, stream, keys, key_bytes, n, (uint64_t)num_rows,
+                       static_cast<uint32_t*>(tab), owner, bits, slot_of, owners, count);
+  } else {
+    hipLaunchKernelGGL(hash_clear_kernel<uint64_t>, dim3((slots / 2 + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint64_t*>(tab), slots, count);
+    hipLaunchKernelGGL(hash_insert_kernel<uint64_t>, dim3((n + kInsertThreads - 1) / kInsertThreads),
+                       dim3(kInsertThreads), 0, stream, keys, key_bytes, n, (uint64_t)num_rows,
+                       static_cast<uint64_t*>(tab), owner, bits, slot_of, owners, count);
+  }
+  // widest vector every row, output row and base is aligned to
+  int vb = 16;
+  while (vb > 1 && (row_bytes % vb || out_stride % vb || (uintptr_t)table % vb || (uintptr_t)out % vb))
+    vb >>= 1;
+  const int64_t nv = row_bytes / vb;
+  int g = 1;
+  while (g < nv && g < 64) g <<= 1;
+  const int passes = (int)((nv + g - 1) / g);
+  int gs = 0;
+  while ((1 << gs) < g) ++gs;
+  constexpr int U = 8;
+  const int tkeys = (64 / g) * U < 64 ? (64 / g) * U : 64;
+  int ts = 0;
+  while ((1 << ts) < tkeys) ++ts;
+  const int64_t waves = (n + tkeys - 1) / tkeys;
+  const int64_t grid = (waves * 64 + 255) / 256;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  HashCopy c{keys, key_bytes, n, table, (uint64_t)row_bytes, slot_of, owner, owners, count,
+             static_cast<uint8_t*>(out), out_stride};
+#define HC(V)                                                                                          \
+  do {                                                                                                 \
+    if (k32)                                                                                           \
+      hipLaunchKernelGGL((hash_copy_kernel<V, U, 0, true>), dim3(grid), dim3(256), 0, stream, c, gs,   \
+                         ts, passes);                                                                  \
+    else                                                                                               \
+      hipLaunchKernelGGL((hash_copy_kernel<V, U, 0, false>), dim3(grid), dim3(256), 0, stream, c, gs,  \
+                         ts, passes);                                                                  \
+    hipLaunchKernelGGL((hash_copy_kernel<V, U, 1, false>), dim3(grid), dim3(256), 0, stream, c, gs,    \
+                       ts, passes);                                                                    \
+  } while (0)
+  switch (vb) {
+    case 16: HC(16); break;
+    case 8: HC(8); break;
+    case 4: HC(4); break;
+    case 2: HC(2); break;
+    default: HC(1); break;
+  }
+#undef HC
+  return hipGetLastError();
 }
 
 hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int flip, uint64_t* k64,

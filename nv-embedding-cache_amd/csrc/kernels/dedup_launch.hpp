@@ -17,4 +17,18 @@ hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const ui
 hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, const uint32_t* u_dev,
                                int key_bytes, void* counts, hipStream_t stream);
 
+// Hash slots for a batch of n keys: a power of two, at least 2n (and 1024).
+size_t hash_dedup_slots(int64_t n);
+// Bytes per hash-table key: 4 when every row index fits 32 bits, else 8.
+size_t hash_dedup_key_bytes(int64_t num_rows);
+// out row i = table row keys[i] for keys in [0, num_rows) (others untouched),
+// deduplicated by hashing.  Scratch: tab (hash_dedup_slots(n) keys of
+// hash_dedup_key_bytes(num_rows) bytes), owner (one word per slot), slot_of
+// (n words), owners (n 8-byte entries), count (one word).  Four launches,
+// asynchronous.
+hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, const uint8_t* table,
+                                    int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride,
+                                    void* tab, uint32_t* owner, uint32_t* slot_of, uint64_t* owners,
+                                    uint32_t* count, hipStream_t stream);
+
 }  // namespace nve_amd

@@ -114,3 +114,53 @@ def test_dedup_gather_int32_and_out_of_range_keys_untouched():
     exp = np.full((keys.size, dim * 4), 0xCD, np.uint8)
     ref, _ = O.gather(keys, np.ascontiguousarray(tb).reshape(-1), dim * 4, rows, out=exp)
     assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("case", ["all_same", "one_key", "odd_width", "strided_out", "distinct"])
+def test_dedup_gather_hash_edge_cases(case):
+    """The hash dedup's corner cases against the oracle gather: every key the
+    same (one owner, every other position copies it), a single key, 6-byte
+    rows (2-byte copies), an output stride wider than the row (the padding
+    untouched), all keys distinct (every position an owner)."""
+    rng = np.random.default_rng(["all_same", "one_key", "odd_width", "strided_out", "distinct"].index(case))
+    rows, dim, n = 4000, 32, 3000
+    width = dim * 2
+    if case == "odd_width":
+        width = 6
+    tb = rng.integers(0, 256, size=(rows, width), dtype=np.uint8)
+    if case == "all_same":
+        keys = np.full(n, 1234, np.int64)
+    elif case == "one_key":
+        keys = np.array([rows - 1], np.int64)
+    elif case == "distinct":
+        keys = rng.permutation(rows)[:n].astype(np.int64)
+    else:
+        keys = rng.integers(0, rows, size=n).astype(np.int64)
+    stride = width + 32 if case == "strided_out" else width
+    d_tab, d_keys = to_dev(tb.reshape(-1)), to_dev(keys)
+    out = torch.full((keys.size, stride), 0x5A, dtype=torch.uint8, device="cuda")
+    ws, wb = workspace(keys.size)
+    ws.fill_(0x77)  # a workspace holding anything (the hash table is cleared by the call)
+    _lib.call("nve_amd_dedup_gather", _lib.KEY_INT64, keys.size, vp(d_keys), vp(d_tab), rows, width, vp(out),
+              stride, vp(ws), wb, stream_ptr())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:, :width], tb[keys])
+    assert np.all(got[:, width:] == 0x5A)
+
+
+def test_dedup_gather_reuses_a_workspace_across_batches():
+    """Two batches through one workspace: the second sees no state of the first."""
+    rng = np.random.default_rng(12)
+    rows, dim = 5000, 16
+    tb = float_table(rng, rows, dim, O.F32)
+    d_tab = to_dev(tb.reshape(-1))
+    ws, wb = workspace(4000)
+    for n in (4000, 1500):
+        keys = rng.integers(0, rows, size=n).astype(np.int64)
+        d_keys = to_dev(keys)
+        out = torch.zeros((n, dim * 4), dtype=torch.uint8, device="cuda")
+        _lib.call("nve_amd_dedup_gather", _lib.KEY_INT64, n, vp(d_keys), vp(d_tab), rows, dim * 4, vp(out),
+                  dim * 4, vp(ws), wb, stream_ptr())
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), np.ascontiguousarray(tb).reshape(rows, -1).view(np.uint8)[keys])
