@@ -228,6 +228,56 @@ def check_pooled_bags(torch, table, keys, out, hot, bag_ids):
     return len(bag_ids)
 
 
+def host_call_costs(torch, lib, calls=400):
+    """Host time per call of one c2pool-shaped pooled lookup (256 bags x 1024
+    keys, CSR offsets, fp16 rows of 128) issued three ways on a 1M-row GPU
+    layer: the NVEmbeddingBag module's forward (an inference layer), the
+    nve_ops torch op (native, dispatcher to C ABI), and the C ABI called
+    through ctypes.  Each way is issued `calls` times without a sync: the host
+    time per call is the issue loop's wall time over `calls`; the GPU time per
+    call comes from events around the same loop.  A way whose host time
+    exceeds its GPU time cannot keep the GPU busy."""
+    import pynve.torch  # noqa: F401  (the native ops library)
+    from pynve.torch.nve_layers import LayerType, NVEmbeddingBag
+    rows, dim, bags, hot = 1_000_000, 128, 256, 1024
+    layer = NVEmbeddingBag(rows, dim, torch.float16, LayerType.GPULayer, "sum", optimize_for_training=False)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    keys = torch.randint(0, rows, (bags * hot,), device="cuda", generator=g)
+    offsets = torch.arange(0, bags * hot + 1, hot, device="cuda")
+    out = torch.empty((bags, dim), dtype=torch.float16, device="cuda")
+    binding = layer.emb_layer
+    stream = torch.cuda.current_stream()
+    ctx = binding._ctx(stream.cuda_stream)
+    look = lib.load().nve_layer_lookup_pooled
+    kp, op, ofp = (ctypes.c_void_p(t.data_ptr()) for t in (keys, out, offsets))
+    ways = {
+        "module_forward": lambda: layer(keys, offsets),
+        "torch_op": lambda: torch.ops.nve_ops.embedding_lookup_with_pooling(
+            layer.marker_tensor, keys, offsets, None, lib.POOL_SUM, dim, layer.dtype_tag),
+        "c_abi_ctypes": lambda: look(binding._layer, ctx, bags * hot, kp, op, dim * 2, None, lib.POOL_SUM,
+                                     lib.SPARSE_CSR, ofp, bags + 1, 0, None, lib.DT_UNKNOWN, lib.DT_F16, None),
+    }
+    res = {}
+    with torch.inference_mode():
+        for name, fn in ways.items():
+            for _ in range(30):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            for _ in range(calls):
+                fn()
+            t1 = time.perf_counter()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            res[name] = {"host_us": round((t1 - t0) / calls * 1e6, 2),
+                         "gpu_us": round(e0.elapsed_time(e1) / calls * 1e3, 2)}
+    del layer
+    return {"shape": "256 bags x 1024 keys (CSR), fp16 x 128, 1M-row GPU layer", "calls": calls, **res}
+
+
 def zipf_ceiling(torch, lib, stream, table, row_bytes, batches, launches=100):
     """Read ceiling on the workload's own keys: the random-row read kernel
     fetching row key[i] of the workload's table for every key of a batch
@@ -302,6 +352,7 @@ def run_workload(args, torch, _lib):
     kgen.manual_seed(1)
     cfg_out = {"workload": w}
     extra = {}
+    traffic_key = w  # profiles/traffic.json entry of this run's kernels, if any
     if w == "c1":
         # BASELINE C1, the reference HostLayer configuration: 1,000,000 x 64 fp32
         # N(0, 0.01); 4,096 bags of 8 keys uniform in [0, 1e6); the Fixed-8 Sum
@@ -439,7 +490,8 @@ def run_workload(args, torch, _lib):
         _lib.call("nve_context_wait", ctx)
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
-        kernel = "sort + gather_kernel" if w == "c2" else "gather_realign_kernel (dequant)"
+        kernel = ("hash dedup + gather: hash_clear, hash_insert, hash_copy (owners), hash_copy (repeats)"
+                  if w == "c2" else "gather_realign_kernel (dequant)")
     elif w == "c3":
         # LinearUVM: pinned host table + 32 GiB 8-way HBM cache, warmed by 10
         # batches (auto-insert), then timed pooled lookups whose misses read the
@@ -582,7 +634,10 @@ def run_workload(args, torch, _lib):
         _lib.call("nve_table_destroy", table)
         hip.hipHostFree(host_ptr)
         kernel = ("gather_kernel / SortGather / PipelineGather (cache + host misses)" if concat
-                  else "pool_kernel (cache + host misses)")
+                  else "pool_split_kernel (cache + host misses)")
+        traffic_key = None  # counters cover the pooled cache kernel only
+        if not concat and args.kernel_mode == 0:
+            traffic_key = "c3_cache_hit" if hit == 1.0 else "c3"
     elif w == "c2bwd":
         # training backprop of the headline lookup: the sparse table gradient of
         # 256 bags x 1024 Zipf(1.05) keys (50M-row range) from a 256 x 128 fp16
@@ -621,7 +676,7 @@ def run_workload(args, torch, _lib):
         cfg_out.update({"table_rows": rows, "dim": dim, "bags": bags, "hotness": hot, "zipf_alpha": alpha,
                         "keys_per_batch": nkeys, "mean_unique_keys": u, "pooling": "sum",
                         "grad_dtype": "f16", "step": "one nve_amd_pooling_backprop call (synchronizes)"})
-        kernel = "dedup sort + backprop_prep + pool_kernel (runs, then per key)"
+        kernel = "radix dedup + backprop_prep + piece_pool_kernel + piece_combine_kernel"
     elif w == "c5":
         T, B, dim = 26, 8192, 128
         cg = torch.Generator()
@@ -670,7 +725,7 @@ def run_workload(args, torch, _lib):
         alg = nkeys * (8 + 4 + dim * 2) + (T * B + 1) * 8 + B * T * dim * 4
         cfg_out.update({"tables": T, "cardinalities": cards, "total_rows": sum(cards), "batch": B,
                         "mean_keys_per_batch": nkeys, "pooling": "weighted_mean", "output_dtype": "f32"})
-        kernel = "pool_kernel (multi-table)"
+        kernel = "pool_short_kernel (multi-table)"
     else:
         raise SystemExit(f"unknown workload {w}")
     achieved = alg / (ms * 1e-3) / 1e9
@@ -681,7 +736,7 @@ def run_workload(args, torch, _lib):
            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
                         "kernel": kernel, "alg_bytes_per_launch": alg}}
-    add_traffic(res["roofline"], w, ms)
+    add_traffic(res["roofline"], traffic_key, ms)
     res.update(extra)
     log(f"{w}: {ms * 1000:.2f} us/step, {res['value'] / 1e9:.2f} G lookups/s, {achieved:.0f} GB/s")
     print(json.dumps(res), flush=True)
@@ -739,6 +794,8 @@ def main():
                     help="c3: GPU table lookup mode (0 auto, 1 LookupUVM, 2 SortGather, 3 PipelineGather)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ceiling", action="store_true")
+    ap.add_argument("--no-host-calls", action="store_true",
+                    help="c2pool: skip the per-call host cost of the module / torch op / C ABI")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run torch's device copy of a 1 GiB buffer 5 times (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -867,6 +924,11 @@ def main():
                              "frac_of_ceiling": round(achieved / c1, 4),
                              "random_row_read_GBps_4x_rows": round(c4, 1),
                              "frac_of_4x_rows_ceiling": round(achieved / c4, 4)}
+    if not args.no_host_calls:
+        hc = host_call_costs(torch, _lib)
+        log("host time per call: " + ", ".join(f"{k} {v['host_us']} us (GPU {v['gpu_us']} us)"
+                                                for k, v in hc.items() if isinstance(v, dict)))
+        result["host_call_us"] = hc
     if not args.no_cpu:
         import numpy as np
         log(f"cpu baseline: copying the table to host ({rows} x {dim} fp16)")

@@ -187,6 +187,10 @@ NVE_C_API nve_status_t nve_amd_pooling_backprop(
  * (include/cuda_support.hpp:26-55). */
 NVE_C_API nve_status_t nve_amd_set_log_level(int32_t level);
 NVE_C_API nve_status_t nve_amd_get_log_level(int32_t* level);
+/* Writes one message through the library's logger if `level` is enabled
+ * (the bindings log hit rates at the perf level this way, as the reference's
+ * binding does with NVE_LOG_PERF_, binding_layers.hpp:370-387). */
+NVE_C_API nve_status_t nve_amd_log_message(int32_t level, const char* message);
 
 #ifdef __cplusplus
 }

@@ -984,6 +984,13 @@ nve_status_t nve_amd_get_log_level(int32_t* level) {
   return NVE_SUCCESS;
 }
 
+nve_status_t nve_amd_log_message(int32_t level, const char* message) {
+  if (level < 0) return set_error(NVE_ERROR_INVALID_ARGUMENT, "log level must not be negative");
+  if (!message) return set_error(NVE_ERROR_INVALID_ARGUMENT, "message must not be NULL");
+  if (log_enabled((LogLevel)level)) log_write((LogLevel)level, message);
+  return NVE_SUCCESS;
+}
+
 nve_status_t nve_amd_read_ceiling(const void* table, int64_t row_size_in_bytes, const int64_t* idx,
                                   int64_t n, uint32_t* sink, void* stream) {
   C_TRY

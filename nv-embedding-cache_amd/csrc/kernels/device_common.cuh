@@ -212,12 +212,17 @@ __device__ __forceinline__ void store_out(uint8_t* p, const float* v, bool out_f
       for (int i = 0; i < E; ++i) o.w[i] = __float_as_uint(v[i]);
       store_vec<4 * E, NT>(p, o);
     } else {
+      // Several 16-byte pieces per lane: each store instruction covers only
+      // part of every line it touches.  Streaming stores send those partial
+      // lines to HBM one by one (the multi-table pool wrote 131,693 KiB for
+      // 106,496 KiB of fp32 output), ordinary stores merge them in L2 first
+      // (exactly 106,496 KiB, same time), so these always go through L2.
 #pragma unroll
       for (int c = 0; c < E / 4; ++c) {
         Vec<16> o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint(v[4 * c + i]);
-        store_vec<16, NT>(p + 16 * c, o);
+        store_vec<16, false>(p + 16 * c, o);
       }
     }
   }

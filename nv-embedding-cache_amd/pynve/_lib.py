@@ -144,6 +144,7 @@ SIGNATURES = {
     "nve_amd_read_ceiling": (I32, [P, I64, P, I64, P, P]),
     "nve_amd_set_log_level": (I32, [I32]),
     "nve_amd_get_log_level": (I32, [P]),
+    "nve_amd_log_message": (I32, [I32, ctypes.c_char_p]),
     "nve_amd_find_and_pool_multi": (I32, [ctypes.c_int, I64, ctypes.POINTER(P), P, I64, I32, I64, I64, P, P,
                                           P, I32, ctypes.c_int, I32, P, P]),
     "nve_amd_dedup_workspace_size": (I32, [I64, ctypes.POINTER(U64)]),

@@ -24,13 +24,10 @@ layer, the parameter-server tables and the multi-process memory blocks
 """
 import ctypes
 import json
-import logging
 import threading
 from enum import IntEnum
 
 from . import _lib
-
-_log = logging.getLogger("pynve")
 
 
 class DataType_t(IntEnum):
@@ -309,9 +306,12 @@ class NVEmbedBinding:
             return ctx
 
     def _log_hit_rates(self, hr):
+        # every logging_interval-th lookup, at the library logger's perf level
+        # (binding_layers.hpp:370-387)
         if self.logging_interval_ > 0:
             if self.logging_counter_ % self.logging_interval_ == 0:
-                _log.info("Hit rates: %s", ", ".join(str(v) for v in hr))
+                msg = "Hit rates: " + ", ".join(f"{v:g}" for v in hr)
+                _lib.call("nve_amd_log_message", 30, msg.encode())
             self.logging_counter_ += 1
 
     def lookup(self, num_keys, keys, output, stream):
@@ -407,7 +407,10 @@ class NVEmbedBinding:
         return out.value
 
     def release_contexts(self):
-        """Wait for and destroy every context (binding_layers.hpp:339-350)."""
+        """Wait for and destroy every context (binding_layers.hpp:339-350),
+        those the native torch ops made for this layer included."""
+        if _native_ops is not None and self._layer is not None:
+            _native_ops.release_layer(self._layer)
         with self._ctx_mu:
             for ctx in self._contexts.values():
                 _lib.call("nve_context_wait", ctx)
@@ -837,16 +840,23 @@ def get_dl_tensor(layer, dtype=None):
 
 _registry = {}
 _registry_mu = threading.Lock()
+# the native ops library's own registry (marker -> layer handle, contexts per
+# stream); pynve.torch installs it when it loads that library
+_native_ops = None
 
 
 def register_for_torch(marker_ptr, binding):
     with _registry_mu:
         _registry[int(marker_ptr)] = binding
+    if _native_ops is not None and getattr(binding, "_layer", None) is not None:
+        _native_ops.register(int(marker_ptr), binding)
 
 
 def unregister_from_torch(marker_ptr):
     with _registry_mu:
         _registry.pop(int(marker_ptr), None)
+    if _native_ops is not None:
+        _native_ops.unregister(int(marker_ptr))
 
 
 def get_binding(marker_ptr):

@@ -1,8 +1,9 @@
 """pynve.torch: torch modules and custom ops over the HIP lookup library.
 
 The two ops of the reference's torch library (torch_binding.cpp:85-92) are
-defined here with the same schemas and implemented for HIP tensors (torch's
-"CUDA" dispatch key on ROCm) and for host tensors ("CPU": host layers):
+defined and implemented natively, in libnve_torch_ops.so (built beside
+libnve_amd.so from csrc/torch_ops/nve_torch_ops.cpp), for HIP tensors (torch's
+"CUDA" dispatch key on ROCm) and host tensors ("CPU": host layers):
 
     nve_ops::embedding_lookup(Tensor marker, Tensor keys, int embedding_size,
                               int dtype) -> Tensor
@@ -10,21 +11,70 @@ defined here with the same schemas and implemented for HIP tensors (torch's
         Tensor offsets, Tensor? weights, int pooling_type, int embedding_size,
         int dtype) -> Tensor
 
-The layer is found through the marker tensor's data_ptr in the binding
-registry (nve_registry.cu:25-50).  Shape inference (the fake kernels) uses
-only the baked `embedding_size` and `dtype` arguments, as the reference's
+Each call goes from the dispatcher straight to the C ABI, with no Python on
+the way.  The layer is found through the marker tensor's data_ptr in the
+library's registry (nve_registry.cu:25-50), which pynve.nve.register_for_torch
+fills.  Shape inference (the fake kernels) uses only the baked
+`embedding_size` and `dtype` arguments, as the reference's
 pynve/torch/__init__.py does.
 """
+import ctypes
+import os
+
 import torch
 
 from .. import nve
+from .._lib import LIB_PATH
 
 HAS_TORCH_OPS = True
 
-_DEF = torch.library.Library("nve_ops", "DEF")
-_DEF.define("embedding_lookup(Tensor marker, Tensor keys, int embedding_size, int dtype) -> Tensor")
-_DEF.define("embedding_lookup_with_pooling(Tensor marker, Tensor keys, Tensor offsets, "
-            "Tensor? weights, int pooling_type, int embedding_size, int dtype) -> Tensor")
+OPS_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libnve_torch_ops.so")
+
+
+class _NativeOps:
+    """ctypes view of the ops library's registry entry points."""
+
+    def __init__(self, path):
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing: build the package (make -C nv-embedding-cache_amd) "
+                              "before importing pynve.torch")
+        torch.ops.load_library(path)  # registers nve_ops::* with the dispatcher
+        lib = ctypes.CDLL(path)
+        P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        self._register = lib.nve_torch_ops_register
+        self._register.argtypes, self._register.restype = [P, P, I64, I32, P, I64], I32
+        self._unregister = lib.nve_torch_ops_unregister
+        self._unregister.argtypes, self._unregister.restype = [P], I32
+        self._release = lib.nve_torch_ops_release_layer
+        self._release.argtypes, self._release.restype = [P], I32
+        self._num_contexts = lib.nve_torch_ops_num_contexts
+        self._num_contexts.argtypes, self._num_contexts.restype = [P, ctypes.POINTER(I64)], I32
+
+    def register(self, marker_ptr, binding):
+        modify = binding._modify_stream.cuda_stream if binding._modify_stream is not None else 0
+        dtype = int(binding.data_type_)
+        if dtype not in (int(nve.DataType_t.Float32), int(nve.DataType_t.Float16)):
+            raise ValueError(f"torch ops serve float32 and float16 layers, not {binding.data_type_!r}")
+        rc = self._register(marker_ptr, binding._layer, binding.row_size_in_bytes_, dtype, modify,
+                            binding.logging_interval_)
+        if rc != 0:
+            raise RuntimeError(f"nve_torch_ops_register refused marker {marker_ptr:#x}")
+
+    def unregister(self, marker_ptr):
+        self._unregister(marker_ptr)
+
+    def release_layer(self, layer):
+        self._release(layer)
+
+    def num_contexts(self, marker_ptr):
+        """Execution contexts the ops made for a marker's layer (one per stream)."""
+        n = ctypes.c_int64()
+        if self._num_contexts(marker_ptr, ctypes.byref(n)) != 0:
+            raise RuntimeError(f"no binding registered for marker_ptr={marker_ptr:#x}")
+        return n.value
+
+
+nve._native_ops = _NativeOps(OPS_LIB_PATH)
 
 
 def _out_dtype(dtype_tag):
@@ -34,74 +84,6 @@ def _out_dtype(dtype_tag):
     if t == nve.DataType_t.Float16:
         return torch.float16
     raise ValueError(f"Invalid data type: {t}")
-
-
-def _check_index_tensor(t, name):
-    # nve_torch_ops_checks.hpp:27-45
-    if t.dtype != torch.int64:
-        raise RuntimeError(f"nve-torch-ops: {name} must be an int64 tensor")
-    if not t.is_contiguous():
-        raise RuntimeError(f"nve-torch-ops: {name} must be contiguous")
-
-
-def _check_pooling_weights(w, num_keys):
-    if not w.is_contiguous():
-        raise RuntimeError("nve-torch-ops: weights must be contiguous")
-    if w.numel() != num_keys:
-        raise RuntimeError("nve-torch-ops: weights must have one element per key")
-    if w.dtype == torch.float32:
-        return int(nve.DataType_t.Float32)
-    if w.dtype == torch.float16:
-        return int(nve.DataType_t.Float16)
-    raise RuntimeError("nve-torch-ops: weights must be a float32 or float16 tensor")
-
-
-def _stream_for(t):
-    """The stream a lookup on tensor t's device runs on (0 for host tensors:
-    a host layer runs on the calling threads)."""
-    return torch.cuda.current_stream(t.device).cuda_stream if t.is_cuda else 0
-
-
-def _embedding_lookup_impl(marker, keys, embedding_size, dtype):
-    """nve_torch_ops.cu:67-98 / nve_torch_ops_cpu.cpp:59-90: [num_keys, dim]
-    rows of the layer's dtype, on the keys' device."""
-    _check_index_tensor(keys, "keys")
-    binding = nve.get_binding(marker.data_ptr())
-    n = keys.numel()
-    out = torch.empty((n, binding.get_embedding_dim()), dtype=_out_dtype(int(binding.get_data_type())),
-                      device=keys.device)
-    binding.lookup(n, keys.data_ptr(), out.data_ptr(), _stream_for(keys))
-    return out
-
-
-def _embedding_lookup_with_pooling_impl(marker, keys, offsets, weights, pooling_type,
-                                        embedding_size, dtype):
-    """nve_torch_ops.cu:100-146 / nve_torch_ops_cpu.cpp:92-133: [num_bags, dim]
-    pooled rows, CSR offsets with num_bags + 1 entries."""
-    _check_index_tensor(keys, "keys")
-    _check_index_tensor(offsets, "offsets")
-    if offsets.numel() < 2:
-        raise RuntimeError("nve-torch-ops: offsets must have at least two entries "
-                           "(num_bags + 1, include_last_offset=True convention)")
-    binding = nve.get_binding(marker.data_ptr())
-    num_bags = offsets.numel() - 1
-    out = torch.empty((num_bags, binding.get_embedding_dim()),
-                      dtype=_out_dtype(int(binding.get_data_type())), device=keys.device)
-    wdt, wptr = int(nve.DataType_t.Unknown), 0
-    if weights is not None:
-        wdt = _check_pooling_weights(weights, keys.numel())
-        wptr = weights.data_ptr()
-    binding.lookup_with_pooling(keys.numel(), keys.data_ptr(), out.data_ptr(), int(pooling_type),
-                                offsets.numel(), offsets.data_ptr(), wdt, wptr, _stream_for(keys))
-    return out
-
-
-# one implementation for both dispatch keys: the binding of the marker decides
-# where the lookup runs (HIP kernels, or CPU threads for a host layer), and
-# buffers on the other side are staged by the layer
-for _key in ("CUDA", "CPU"):
-    _DEF.impl("embedding_lookup", _embedding_lookup_impl, _key)
-    _DEF.impl("embedding_lookup_with_pooling", _embedding_lookup_with_pooling_impl, _key)
 
 
 @torch.library.register_fake("nve_ops::embedding_lookup")

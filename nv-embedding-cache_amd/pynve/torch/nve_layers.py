@@ -308,15 +308,18 @@ class NVEmbeddingBase(torch.nn.Module):
         if self.optimize_for_training:
             return nve_ops.NVEmbeddingOpTraining.apply(self.marker_tensor, keys, self.weight,
                                                        self.embedding_size, self.dtype_tag)
-        return nve_ops.NVEmbeddingOp.apply(self.marker_tensor, keys, self.embedding_size, self.dtype_tag)
+        # an inference layer's op takes no weight, so its output has no autograd
+        # history: call the op itself and spare the autograd.Function's cost
+        return torch.ops.nve_ops.embedding_lookup(self.marker_tensor, keys, self.embedding_size, self.dtype_tag)
 
     def _bags(self, keys, offsets, per_sample_weights, pooling_type):
         if self.optimize_for_training:
             return nve_ops.NVEmbeddingBagOpTraining.apply(self.marker_tensor, keys, self.weight, offsets,
                                                           per_sample_weights, pooling_type,
                                                           self.embedding_size, self.dtype_tag)
-        return nve_ops.NVEmbeddingBagOp.apply(self.marker_tensor, keys, offsets, per_sample_weights,
-                                              pooling_type, self.embedding_size, self.dtype_tag)
+        return torch.ops.nve_ops.embedding_lookup_with_pooling(self.marker_tensor, keys, offsets,
+                                                               per_sample_weights, pooling_type,
+                                                               self.embedding_size, self.dtype_tag)
 
 
 class NVEmbedding(NVEmbeddingBase):
