@@ -11,7 +11,10 @@ batch; batches are generated up front and stay resident in HBM.
 Reported beside the throughput:
   roofline      algorithmic bytes per launch / the kernel's mean duration
                 (HIP events on the lookup stream) against the 8 TB/s HBM peak,
-                and against the measured random-row read ceiling;
+                and the HBM bytes rocprofv3 counts per launch over the same
+                time (frac_dram); beside it a plain row-read kernel's rate on
+                the same keys and on uniform keys, for comparison;
+  host_call_us  host time per call of the module, the torch op and the C ABI;
   cpu_baseline  the product's CPU HostLayer (threaded gather + fp32 pooling,
                 restating the reference's) timed on this host's cores on
                 whole batches of the same workload, median with p10 / p90,
@@ -153,8 +156,8 @@ def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, s
 
 
 def read_ceiling(torch, lib, stream, counts):
-    """Random-row read ceiling: uniform random 256-byte rows of a 16 GiB buffer
-    (far beyond the 256 MB MALL), read by a kernel that does nothing else.
+    """Plain row-read kernel on uniform random 256-byte rows of a 16 GiB buffer
+    (far beyond the 256 MB MALL), reading and folding the rows and nothing else.
     Returns {rows_per_launch: (GB/s, us per launch)}."""
     row_bytes = 256
     rows = (16 << 30) // row_bytes
@@ -167,9 +170,14 @@ def read_ceiling(torch, lib, stream, counts):
         idx = torch.randint(0, rows, (n,), device="cuda", generator=gen, dtype=torch.int64)
         sink = torch.zeros((n + 127) // 128, dtype=torch.int32, device="cuda")
 
+        fn = lib.load().nve_amd_read_ceiling  # resolved once: the issue loop stays below the kernel time
+        args = (ctypes.c_void_p(buf.data_ptr()), row_bytes, ctypes.c_void_p(idx.data_ptr()), n,
+                ctypes.c_void_p(sink.data_ptr()), s)
+
         def launch():
-            lib.call("nve_amd_read_ceiling", ctypes.c_void_p(buf.data_ptr()), row_bytes,
-                     ctypes.c_void_p(idx.data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
+            st = fn(*args)
+            if st:
+                lib.check(st)
 
         for _ in range(5):
             launch()
@@ -279,16 +287,21 @@ def host_call_costs(torch, lib, calls=400):
 
 
 def zipf_ceiling(torch, lib, stream, table, row_bytes, batches, launches=100):
-    """Read ceiling on the workload's own keys: the random-row read kernel
+    """Plain row-read kernel on the workload's own keys: the random-row read kernel
     fetching row key[i] of the workload's table for every key of a batch
     (same rows, same L2/MALL reuse, no pooling), cycling the batches."""
     sink = torch.zeros((batches[0].numel() + 127) // 128, dtype=torch.int32, device="cuda")
     s = ctypes.c_void_p(stream.cuda_stream)
     n = batches[0].numel()
 
+    fn = lib.load().nve_amd_read_ceiling  # resolved once, arguments built once per batch
+    args = [(ctypes.c_void_p(table.data_ptr()), row_bytes, ctypes.c_void_p(b.data_ptr()), n,
+             ctypes.c_void_p(sink.data_ptr()), s) for b in batches]
+
     def launch(i):
-        lib.call("nve_amd_read_ceiling", ctypes.c_void_p(table.data_ptr()), row_bytes,
-                 ctypes.c_void_p(batches[i % len(batches)].data_ptr()), n, ctypes.c_void_p(sink.data_ptr()), s)
+        st = fn(*args[i % len(args)])
+        if st:
+            lib.check(st)
 
     ms = time_steps(torch, stream, launch, 5, launches)
     return (n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms * 1e3
@@ -379,14 +392,21 @@ def run_workload(args, torch, _lib):
         _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
         kp = [ctypes.c_void_p(b.data_ptr()) for b in batches]
 
+        # arguments built once: a ~4 us kernel would otherwise wait on the issue loop
+        pooled_args = [(layer, ctx, nkeys, k, ctypes.c_void_p(pooled.data_ptr()), width, None, _lib.POOL_SUM,
+                        _lib.SPARSE_FIXED, None, 0, hot, None, _lib.DT_UNKNOWN, _lib.DT_F32, None) for k in kp]
+        plain_args = [(layer, ctx, nkeys, k, ctypes.c_void_p(gathered.data_ptr()), width, None, None) for k in kp]
+        pooled_fn, plain_fn = L.nve_layer_lookup_pooled, L.nve_layer_lookup
+
         def step(i):
-            _lib.check(L.nve_layer_lookup_pooled(layer, ctx, nkeys, kp[i % len(kp)], ctypes.c_void_p(pooled.data_ptr()),
-                                                 width, None, _lib.POOL_SUM, _lib.SPARSE_FIXED, None, 0, hot, None,
-                                                 _lib.DT_UNKNOWN, _lib.DT_F32, None))
+            st = pooled_fn(*pooled_args[i % len(kp)])
+            if st:
+                _lib.check(st)
 
         def plain(i):
-            _lib.check(L.nve_layer_lookup(layer, ctx, nkeys, kp[i % len(kp)], ctypes.c_void_p(gathered.data_ptr()),
-                                          width, None, None))
+            st = plain_fn(*plain_args[i % len(kp)])
+            if st:
+                _lib.check(st)
 
         ms_plain = time_steps(torch, stream, plain, args.warmup, args.steps)
         ms = time_steps(torch, stream, step, args.warmup, args.steps)
@@ -635,9 +655,9 @@ def run_workload(args, torch, _lib):
         hip.hipHostFree(host_ptr)
         kernel = ("gather_kernel / SortGather / PipelineGather (cache + host misses)" if concat
                   else "pool_split_kernel (cache + host misses)")
-        traffic_key = None  # counters cover the pooled cache kernel only
-        if not concat and args.kernel_mode == 0:
-            traffic_key = "c3_cache_hit" if hit == 1.0 else "c3"
+        # HBM counters only for the all-hit case: with misses the kernel is bound by
+        # the host link, whose reads the same counters mix in
+        traffic_key = "c3_cache_hit" if hit == 1.0 and not concat and args.kernel_mode == 0 else None
     elif w == "c2bwd":
         # training backprop of the headline lookup: the sparse table gradient of
         # 256 bags x 1024 Zipf(1.05) keys (50M-row range) from a 256 x 128 fp16
@@ -911,19 +931,22 @@ def main():
               "step_spread": spread,
               "roofline": roof}
     if not args.no_ceiling:
+        # A plain read kernel (rows read and folded, nothing pooled) on the same
+        # keys and table, and on uniform keys over 16 GiB.  It reads the Zipf
+        # batch slower than the pool kernel does (10.9 vs 8.3 us, also with 16
+        # or 32 rows in flight per lane group or a chunked layout), so it bounds
+        # nothing: the physical fraction is frac_dram (counted HBM bytes).
         zc, zus = zipf_ceiling(torch, _lib, stream, d_table, width, batches)
-        log(f"read ceiling on the workload's own keys and table: {zc:.0f} GB/s ({zus:.1f} us per batch)")
-        roof["zipf_read_ceiling_GBps"] = round(zc, 1)
-        roof["frac_of_zipf_ceiling"] = round(achieved / zc, 4)
+        log(f"read kernel on the workload's own keys and table: {zc:.0f} GB/s ({zus:.1f} us per batch)")
+        roof["zipf_read_kernel_GBps"] = round(zc, 1)
+        roof["vs_zipf_read_kernel"] = round(achieved / zc, 4)
         # same number of rows per launch as one batch, and 4x that (closer to asymptotic)
         c = read_ceiling(torch, _lib, stream, [nkeys, 4 * nkeys])
         (c1, us1), (c4, us4) = c[nkeys], c[4 * nkeys]
-        log(f"random-row read ceiling: {c1:.0f} GB/s at {nkeys} rows/launch ({us1:.1f} us), "
+        log(f"uniform random-row read kernel: {c1:.0f} GB/s at {nkeys} rows/launch ({us1:.1f} us), "
             f"{c4:.0f} GB/s at {4 * nkeys} rows/launch ({us4:.1f} us)")
-        result["ceiling"] = {"random_row_read_GBps": round(c1, 1), "rows_per_launch": nkeys,
-                             "frac_of_ceiling": round(achieved / c1, 4),
-                             "random_row_read_GBps_4x_rows": round(c4, 1),
-                             "frac_of_4x_rows_ceiling": round(achieved / c4, 4)}
+        result["uniform_read_kernel"] = {"GBps": round(c1, 1), "rows_per_launch": nkeys, "us": round(us1, 2),
+                                         "GBps_4x_rows": round(c4, 1), "us_4x_rows": round(us4, 2)}
     if not args.no_host_calls:
         hc = host_call_costs(torch, _lib)
         log("host time per call: " + ", ".join(f"{k} {v['host_us']} us (GPU {v['gpu_us']} us)"

@@ -104,9 +104,9 @@ NVE_C_API nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int
                                                     int64_t num_rows, int64_t row_size_in_bytes,
                                                     void* output, int64_t output_stride, void* stream);
 
-/* Random-row read ceiling microbenchmark: reads row idx[i] (row_size_in_bytes
- * each, a multiple of 16) of a device table for i < n and folds the bytes into
- * sink (one uint32 per 256-thread workgroup, ceil(n/128) words). */
+/* Random-row read microbenchmark: reads row idx[i] (row_size_in_bytes each, a
+ * multiple of 16) of a device table for i < n and folds the bytes into sink
+ * (one uint32 per 256-thread workgroup, ceil(n/128) words). */
 NVE_C_API nve_status_t nve_amd_read_ceiling(const void* table, int64_t row_size_in_bytes,
                                             const int64_t* idx, int64_t n, uint32_t* sink,
                                             void* stream);
