@@ -86,7 +86,7 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
                              const void* offsets, int64_t num_bags, int64_t hotness,
                              const void* weights, int wdt, const void* grads_in, int gdt,
                              int64_t dim, void* unique_out, void* grads_out, void* ws,
-                             size_t ws_bytes, hipStream_t s) {
+                             size_t ws_bytes, hipStream_t s, bool exact) {
   if (n <= 0) return 0;
   NVE_CHECK_ARG(key_bytes == 4 || key_bytes == 8, "Unsupported key size ", key_bytes);
   NVE_CHECK_ARG(gdt == kF32 || gdt == kF16, "Gradients must be float32 or float16");
@@ -118,9 +118,9 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
 
   // (1) dedup: unique keys straight into the caller's buffer
   // (the unique count is read once everything is queued: no stall in between)
-  const uint32_t* u_dev = nullptr;
+  const DedupHead* head_dev = nullptr;
   dedup_run(key_bytes, n, keys, unique_out, b.counts, b.inverse, b.doff, b.dedup_ws, b.dedup_bytes, s,
-            b.kidx, &u_dev);
+            b.kidx, &head_dev, exact);
 
   // (2) gradient row and weight per dedup position
   if (mode == kBackpropMean || mode == kBackpropWMean)
@@ -147,7 +147,11 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
   const int weighted = (mode == kBackpropWSum || mode == kBackpropMean || mode == kBackpropWMean) ? 1 : 0;
   NVE_HIP(launch_piece_pool(a, f16, weighted, s));
   NVE_HIP(launch_piece_combine(a, f16, s));
-  return (int64_t)read_back(u_dev, s);
+  const DedupHead h = read_back(head_dev, s);
+  if (!exact && dedup_spec_failed(h))  // keys differ above the speculated sort bits: all again, exactly
+    return pooling_backprop_run(key_bytes, n, keys, pooling, sparse, offsets, num_bags, hotness, weights, wdt,
+                                grads_in, gdt, dim, unique_out, grads_out, ws, ws_bytes, s, true);
+  return (int64_t)h.total;
 }
 
 }  // namespace nve_amd

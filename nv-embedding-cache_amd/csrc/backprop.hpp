@@ -18,6 +18,6 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
                              const void* offsets, int64_t num_bags, int64_t hotness,
                              const void* weights, int wdt, const void* grads_in, int gdt,
                              int64_t dim, void* unique_out, void* grads_out, void* ws,
-                             size_t ws_bytes, hipStream_t s);
+                             size_t ws_bytes, hipStream_t s, bool exact = false);
 
 }  // namespace nve_amd

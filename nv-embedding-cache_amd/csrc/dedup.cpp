@@ -22,8 +22,8 @@ int bits_for(uint64_t max_value) {
 }
 
 struct DedupBufs {
-  unsigned long long* span;
-  uint32_t* total;
+  DedupHead* head;
+  uint64_t* span_part;
   uint64_t *ka, *kb;
   uint32_t *va, *vb, *heads, *start;
   void* sort_tmp;
@@ -34,10 +34,10 @@ size_t pad(size_t b) { return (b + 255) / 256 * 256; }
 DedupBufs carve(void* ws, int64_t n) {
   uint8_t* p = static_cast<uint8_t*>(ws);
   DedupBufs d;
-  d.span = reinterpret_cast<unsigned long long*>(p);
+  d.head = reinterpret_cast<DedupHead*>(p);
   p += 256;
-  d.total = reinterpret_cast<uint32_t*>(p);
-  p += 256;
+  d.span_part = reinterpret_cast<uint64_t*>(p);
+  p += pad(8 * (size_t)dedup_span_parts(n));
   d.ka = reinterpret_cast<uint64_t*>(p);
   p += pad(8 * n);
   d.kb = reinterpret_cast<uint64_t*>(p);
@@ -67,39 +67,64 @@ constexpr int64_t kHashGatherMaxKeys = int64_t(1) << 30;
 
 size_t dedup_workspace_bytes(int64_t n) {
   if (n < 1) n = 1;
-  const size_t sort = 512 + 2 * pad(8 * n) + 4 * pad(4 * n) + pad(4 * (n + 1)) + radix_sort_temp_bytes(n);
+  const size_t sort = 256 + pad(8 * (size_t)dedup_span_parts(n)) + 2 * pad(8 * n) + 4 * pad(4 * n) +
+                      pad(4 * (n + 1)) + radix_sort_temp_bytes(n);
   const size_t hash = n <= kHashGatherMaxKeys ? hash_gather_bytes(n) : 0;
   return sort > hash ? sort : hash;
 }
 
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
                   void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
-                  uint32_t* pos_key, const uint32_t** count_dev) {
+                  uint32_t* pos_key, const DedupHead** head_dev, bool exact) {
   if (n <= 0) return 0;
   NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
   NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
   DedupBufs b = carve(ws, n);
-  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, s));
-  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(b.span), 1, 0, s));
-  NVE_HIP(key_span(b.ka, n, b.span, s));
-  const unsigned long long span = read_back(b.span, s);
+  int bits = kSpecSortBits;
+  if (exact) {
+    NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, nullptr, s));
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(&b.head->span), 1, 0, s));
+    NVE_HIP(key_span(b.ka, n, &b.head->span, s));
+    bits = bits_for(read_back(&b.head->span, s));
+  } else {
+    // the span is reduced on the way (prep's parts, outputs' workgroup 0) and
+    // checked by whoever reads the head
+    NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, b.span_part, s));
+  }
   int alt = 0;
-  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, bits_for(span), b.sort_tmp,
-                           &alt, s));
+  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, bits, b.sort_tmp, &alt, s));
   const uint64_t* ks = alt ? b.kb : b.ka;
   const uint32_t* vs = alt ? b.vb : b.va;
+  if (run_blocks(n) <= kRunMaxBlocks) {
+    // every output in two launches (block scratch in the heads / start arrays)
+    NVE_HIP(launch_dedup_runs(ks, vs, n, key_bytes, unique, counts, inverse, offsets, pos_key, &b.head->total,
+                              b.heads, reinterpret_cast<int64_t*>(b.start), exact ? nullptr : b.span_part,
+                              exact ? nullptr : &b.head->span, s));
+    if (head_dev != nullptr) {
+      *head_dev = b.head;
+      return -1;
+    }
+    const DedupHead h = read_back(b.head, s);
+    if (!exact && dedup_spec_failed(h))
+      return dedup_run(key_bytes, n, keys, unique, counts, inverse, offsets, ws, ws_bytes, s, pos_key, nullptr,
+                       true);
+    return (int64_t)h.total;
+  }
   NVE_HIP(launch_run_heads(ks, n, b.heads, s));
-  NVE_HIP(exclusive_scan_u32(b.heads, n, b.total, b.sort_tmp, s));
-  NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start,
-                               pos_key, s));
-  if (count_dev != nullptr) {  // the caller reads the count when it needs it
-    NVE_HIP(launch_dedup_counts(b.start, (uint32_t)n, b.total, key_bytes, counts, s));
-    *count_dev = b.total;
+  NVE_HIP(exclusive_scan_u32(b.heads, n, &b.head->total, b.sort_tmp, s));
+  NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, pos_key,
+                               exact ? nullptr : b.span_part, exact ? nullptr : &b.head->span, s));
+  if (head_dev != nullptr) {  // the caller reads the head when it needs it
+    NVE_HIP(launch_dedup_counts(b.start, (uint32_t)n, &b.head->total, key_bytes, counts, s));
+    *head_dev = b.head;
     return -1;
   }
-  const uint32_t u = read_back(b.total, s);
-  NVE_HIP(launch_dedup_counts(b.start, u, nullptr, key_bytes, counts, s));
-  return (int64_t)u;
+  const DedupHead h = read_back(b.head, s);
+  if (!exact && dedup_spec_failed(h))
+    return dedup_run(key_bytes, n, keys, unique, counts, inverse, offsets, ws, ws_bytes, s, pos_key, nullptr,
+                     true);
+  NVE_HIP(launch_dedup_counts(b.start, h.total, nullptr, key_bytes, counts, s));
+  return (int64_t)h.total;
 }
 
 void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t* table,
@@ -128,7 +153,7 @@ void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t*
   DedupBufs b = carve(ws, n);
   // rows of [0, num_rows): sort on the row-index bits only (keys outside the
   // table stay unresolved and their output rows untouched)
-  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, s));
+  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, nullptr, s));
   int alt = 0;
   NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0,
                            bits_for((uint64_t)(num_rows > 1 ? num_rows - 1 : 1)),

@@ -1,11 +1,13 @@
 // dedup.hip -- key deduplication on the GPU (Deduper::dedup, deduper.cuh:136-221)
 // and the dedup-then-gather.
 //
-// dedup: stable radix sort of (key, position) -> run heads -> exclusive scan
-// -> per run: unique key, start offset; per position: inverse = original
-// position in key order; counts from consecutive starts.  Outputs match the
-// reference's: unique keys ascending (signed order), counts, the stable
-// inverse map and exclusive offsets.
+// dedup: stable radix sort of (key, position) -> runs of equal keys -> per
+// run: unique key, start offset, count; per position: inverse = original
+// position in key order.  The runs take two launches (per-block head counts,
+// then every output with the blocks before as carry-in) up to kRunMaxBlocks
+// blocks, else run heads -> exclusive scan -> outputs -> counts.  Outputs
+// match the reference's: unique keys ascending (signed order), counts, the
+// stable inverse map and exclusive offsets.
 //
 // dedup-then-gather needs no order, so it dedups by hashing instead of
 // sorting (four launches instead of eleven): every distinct key of a
@@ -19,23 +21,56 @@
 
 namespace nve_amd {
 
+// OR of x over the 256 threads of the workgroup, in every thread (all threads call it)
+__device__ __forceinline__ uint64_t block_or(uint64_t x) {
+  __shared__ uint64_t red[4];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x |= __shfl_xor(x, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  return red[0] | red[1] | red[2] | red[3];
+}
+
+// span_part (optional): span_part[b] = OR over workgroup b's keys of
+// key ^ key[0] (sort keys), the bits where they differ from the first key.
 __global__ __launch_bounds__(256) void dedup_prep_kernel(const void* keys, int key_bytes, int64_t n,
-                                                         int flip, uint64_t* k64, uint32_t* v) {
+                                                         int flip, uint64_t* k64, uint32_t* v,
+                                                         uint64_t* span_part) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint64_t diff = 0;
   if (i < n) {
     const int64_t k = load_key(keys, key_bytes, i);
-    k64[i] = flip ? flip_key(k, key_bytes) : (uint64_t)k;
+    const uint64_t kk = flip ? flip_key(k, key_bytes) : (uint64_t)k;
+    k64[i] = kk;
     v[i] = (uint32_t)i;
+    if (span_part != nullptr) {
+      const int64_t k0 = load_key(keys, key_bytes, 0);
+      diff = kk ^ (flip ? flip_key(k0, key_bytes) : (uint64_t)k0);
+    }
+  }
+  if (span_part != nullptr) {  // uniform: the whole workgroup reduces
+    const uint64_t d = block_or(diff);
+    if (threadIdx.x == 0) span_part[blockIdx.x] = d;
   }
 }
 
 // inverse[i] = position of the i-th key in key order; at a run head:
 // unique[u] = key, offsets[u] = i (= start[u]); start[U] = n.
+// span_part (optional, nparts words): workgroup 0 also ORs the prep's span
+// parts into *span_out.
 __global__ __launch_bounds__(256) void dedup_outputs_kernel(const uint64_t* ks, const uint32_t* vs,
                                                             const uint32_t* scan, int64_t n,
                                                             int key_bytes, void* unique,
                                                             void* inverse, void* offsets,
-                                                            uint32_t* start, uint32_t* pos_key) {
+                                                            uint32_t* start, uint32_t* pos_key,
+                                                            const uint64_t* span_part, int64_t nparts,
+                                                            unsigned long long* span_out) {
+  if (span_part != nullptr && blockIdx.x == 0) {  // uniform over the workgroup
+    uint64_t a = 0;
+    for (int64_t j = threadIdx.x; j < nparts; j += blockDim.x) a |= span_part[j];
+    a = block_or(a);
+    if (threadIdx.x == 0) *span_out = a;
+  }
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   store_key(inverse, key_bytes, i, (int64_t)vs[i]);
@@ -58,6 +93,186 @@ __global__ __launch_bounds__(256) void dedup_counts_kernel(const uint32_t* start
   const uint32_t u = blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t m = u_dev != nullptr ? *u_dev : u_n;
   if (u < m) store_key(counts, key_bytes, u, (int64_t)(start[u + 1] - start[u]));
+}
+
+// ---------------------------------------------------------------------------
+// runs of the sorted keys in two launches (batches of up to kRunMaxBlocks
+// blocks of kRunBlock keys): run_block_kernel counts each block's run heads
+// and notes its last head; run_outputs_kernel takes the sums and maxima of
+// the blocks before its own as carry-in (so no scan launch sits between), and
+// writes every output of the dedup: per position its inverse entry and unique
+// index, per run its key and offset at the head and its count at the tail.
+// ---------------------------------------------------------------------------
+constexpr int kRunThreads = 256;
+constexpr int kRunItems = 4;
+constexpr int kRunBlock = kRunThreads * kRunItems;
+
+// Block-wide exclusive sum of c and exclusive maximum of l over thread order
+// (every thread calls it); *sum = the block's total of c.
+__device__ __forceinline__ void block_scan_sum_max(uint32_t c, int64_t l, uint32_t* ex_c, int64_t* ex_l,
+                                                   uint32_t* sum) {
+  __shared__ uint32_t wc[kRunThreads / 64];
+  __shared__ int64_t wl[kRunThreads / 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t ic = c;  // inclusive within the wave
+  int64_t il = l;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t pc = __shfl_up(ic, o);
+    const int64_t pl = __shfl_up(il, o);
+    if (lane >= o) {
+      ic += pc;
+      il = pl > il ? pl : il;
+    }
+  }
+  if (lane == 63) {
+    wc[wave] = ic;
+    wl[wave] = il;
+  }
+  __syncthreads();
+  uint32_t bc = 0;
+  int64_t bl = -1;
+  for (int w = 0; w < wave; ++w) {
+    bc += wc[w];
+    bl = wl[w] > bl ? wl[w] : bl;
+  }
+  uint32_t tot = 0;
+  for (int w = 0; w < kRunThreads / 64; ++w) tot += wc[w];
+  // exclusive: inclusive minus own, maximum of the lanes before
+  const int64_t prev_l = __shfl_up(il, 1);
+  *ex_c = bc + ic - c;
+  const int64_t lane_l = lane > 0 ? prev_l : -1;
+  *ex_l = lane_l > bl ? lane_l : bl;
+  *sum = tot;
+}
+
+// blk_count[b] = run heads in block b, blk_last[b] = its last head position (-1: none)
+__global__ __launch_bounds__(kRunThreads) void run_block_kernel(const uint64_t* ks, int64_t n,
+                                                                uint32_t* blk_count, int64_t* blk_last) {
+  const int64_t base = (int64_t)blockIdx.x * kRunBlock;
+  uint32_t c = 0;
+  int64_t l = -1;
+#pragma unroll 4
+  for (int j = 0; j < kRunItems; ++j) {
+    const int64_t i = base + (int64_t)j * kRunThreads + threadIdx.x;  // coalesced
+    if (i < n && (i == 0 || ks[i] != ks[i - 1])) {
+      ++c;
+      l = i;
+    }
+  }
+  uint32_t ex_c, sum;
+  int64_t ex_l;
+  block_scan_sum_max(c, l, &ex_c, &ex_l, &sum);
+  // the block's last head: the maximum over all threads
+  __shared__ int64_t last;
+  if (threadIdx.x == kRunThreads - 1) last = l > ex_l ? l : ex_l;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    blk_count[blockIdx.x] = sum;
+    blk_last[blockIdx.x] = last;
+  }
+}
+
+struct RunOutputs {
+  const uint64_t* ks;
+  const uint32_t* vs;
+  int64_t n;
+  const uint32_t* blk_count;
+  const int64_t* blk_last;
+  int key_bytes;
+  void* unique;
+  void* counts;
+  void* inverse;
+  void* offsets;
+  uint32_t* pos_key;   // optional
+  uint32_t* total;     // the unique count, written by the last block
+  const uint64_t* span_part;  // optional: block 0 ORs these into *span_out
+  int64_t nparts;
+  unsigned long long* span_out;
+};
+
+__global__ __launch_bounds__(kRunThreads) void run_outputs_kernel(RunOutputs a) {
+  if (a.span_part != nullptr && blockIdx.x == 0) {  // uniform over the workgroup
+    uint64_t x = 0;
+    for (int64_t j = threadIdx.x; j < a.nparts; j += blockDim.x) x |= a.span_part[j];
+    x = block_or(x);
+    if (threadIdx.x == 0) *a.span_out = x;
+  }
+  // carry-in: heads before this block, and the last head before it
+  uint32_t u0;
+  int64_t h0;
+  {
+    __shared__ uint32_t in_c[kRunThreads / 64];
+    __shared__ int64_t in_l[kRunThreads / 64];
+    uint32_t c = 0;
+    int64_t l = -1;
+    for (uint32_t b = threadIdx.x; b < blockIdx.x; b += blockDim.x) {
+      c += a.blk_count[b];
+      l = a.blk_last[b] > l ? a.blk_last[b] : l;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      c += __shfl_xor(c, o);
+      const int64_t p = __shfl_xor(l, o);
+      l = p > l ? p : l;
+    }
+    if ((threadIdx.x & 63) == 0) {
+      in_c[threadIdx.x >> 6] = c;
+      in_l[threadIdx.x >> 6] = l;
+    }
+    __syncthreads();
+    u0 = 0;
+    h0 = -1;
+#pragma unroll
+    for (int w = 0; w < kRunThreads / 64; ++w) {
+      u0 += in_c[w];
+      h0 = in_l[w] > h0 ? in_l[w] : h0;
+    }
+  }
+
+  // this thread's kRunItems consecutive positions
+  const int64_t first = (int64_t)blockIdx.x * kRunBlock + (int64_t)threadIdx.x * kRunItems;
+  uint64_t k[kRunItems];
+#pragma unroll
+  for (int j = 0; j < kRunItems; ++j) k[j] = first + j < a.n ? a.ks[first + j] : 0;
+  const uint64_t before = first > 0 && first - 1 < a.n ? a.ks[first - 1] : 0;
+  const uint64_t after = first + kRunItems < a.n ? a.ks[first + kRunItems] : 0;
+  uint32_t c = 0;
+  int64_t l = -1;
+#pragma unroll
+  for (int j = 0; j < kRunItems; ++j) {
+    const int64_t i = first + j;
+    const bool head = i < a.n && (i == 0 || k[j] != (j ? k[j - 1] : before));
+    if (head) {
+      ++c;
+      l = i;
+    }
+  }
+  uint32_t ex_c, sum;
+  int64_t ex_l;
+  block_scan_sum_max(c, l, &ex_c, &ex_l, &sum);
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *a.total = u0 + sum;
+
+  // the run in progress at this thread's first position
+  uint32_t u = u0 + ex_c - 1u;  // wraps for position 0, which is a head
+  int64_t start = ex_l > h0 ? ex_l : h0;
+#pragma unroll
+  for (int j = 0; j < kRunItems; ++j) {
+    const int64_t i = first + j;
+    if (i >= a.n) break;
+    const bool head = i == 0 || k[j] != (j ? k[j - 1] : before);
+    if (head) {
+      ++u;
+      start = i;
+      store_key(a.unique, a.key_bytes, u, unflip_key(k[j], a.key_bytes));
+      store_key(a.offsets, a.key_bytes, u, i);
+    }
+    store_key(a.inverse, a.key_bytes, i, (int64_t)a.vs[i]);
+    if (a.pos_key != nullptr) a.pos_key[i] = u;
+    const bool tail = i == a.n - 1 || k[j] != (j + 1 < kRunItems ? k[j + 1] : after);
+    if (tail) store_key(a.counts, a.key_bytes, u, i + 1 - start);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -338,21 +553,41 @@ hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, 
   return hipGetLastError();
 }
 
+int64_t dedup_span_parts(int64_t n) { return n > 0 ? (n + 255) / 256 : 0; }
+
 hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int flip, uint64_t* k64,
-                             uint32_t* v, hipStream_t stream) {
+                             uint32_t* v, uint64_t* span_part, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(dedup_prep_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, keys, key_bytes,
-                     n, flip, k64, v);
+                     n, flip, k64, v, span_part);
   return hipGetLastError();
 }
 
 hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan,
                                 int64_t n, int key_bytes, void* unique, void* inverse,
                                 void* offsets, uint32_t* start, uint32_t* pos_key,
+                                const uint64_t* span_part, unsigned long long* span_out,
                                 hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(dedup_outputs_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, vs, scan,
-                     n, key_bytes, unique, inverse, offsets, start, pos_key);
+                     n, key_bytes, unique, inverse, offsets, start, pos_key, span_part,
+                     dedup_span_parts(n), span_out);
+  return hipGetLastError();
+}
+
+int64_t run_blocks(int64_t n) { return (n + kRunBlock - 1) / kRunBlock; }
+
+hipError_t launch_dedup_runs(const uint64_t* ks, const uint32_t* vs, int64_t n, int key_bytes, void* unique,
+                             void* counts, void* inverse, void* offsets, uint32_t* pos_key, uint32_t* total,
+                             uint32_t* blk_count, int64_t* blk_last, const uint64_t* span_part,
+                             unsigned long long* span_out, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t nb = run_blocks(n);
+  if (nb > kRunMaxBlocks) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(run_block_kernel, dim3(nb), dim3(kRunThreads), 0, stream, ks, n, blk_count, blk_last);
+  RunOutputs a{ks, vs, n, blk_count, blk_last, key_bytes, unique, counts, inverse, offsets, pos_key, total,
+               span_part, dedup_span_parts(n), span_out};
+  hipLaunchKernelGGL(run_outputs_kernel, dim3(nb), dim3(kRunThreads), 0, stream, a);
   return hipGetLastError();
 }
 

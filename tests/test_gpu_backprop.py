@@ -98,6 +98,30 @@ def test_backprop_matches_oracle_bitwise(pooling, sparse, key_dtype, gdt):
     assert np.array_equal(out, rout.view(bits))
 
 
+@pytest.mark.parametrize("case", ["high_common_bits", "bit_27_outlier", "negative_int32"])
+def test_key_spans_beyond_the_assumed_sort_bits(case):
+    """The dedup inside the backprop first sorts on the low 27 bits and reads
+    the key span with the unique count; keys that differ higher up (an outlier
+    with bit 27 set, negative int32 keys) are run again on their exact bits,
+    keys that only share high bits are not.  Sum over Fixed bags, fp32."""
+    rng = np.random.default_rng(127)
+    bags, hot, dim = 96, 32, 64
+    n = bags * hot
+    keys = rng.zipf(1.2, size=n) % 3000
+    if case == "high_common_bits":
+        keys = (keys + 2**40).astype(np.int64)
+    elif case == "bit_27_outlier":
+        keys = keys.astype(np.int64)
+        keys[n // 3] = 2**27 + 5
+    else:
+        keys = (keys - 1500).astype(np.int32)
+    g = rng.normal(0, 1, size=(bags, dim)).astype(np.float32)
+    uq, out = gpu_backprop(keys, O.SUM, O.FIXED, None, hot, None, O.F32, g, O.F32, dim)
+    ruq, rout = O.pooling_backprop(keys, O.SUM, O.FIXED, None, bags, hot, None, O.F32, g, O.F32, dim)
+    assert np.array_equal(uq, ruq)
+    assert np.array_equal(out, rout.view(np.uint32))
+
+
 def test_positions_outside_bags_and_empty_input():
     rng = np.random.default_rng(431)
     rows, dim, bags = 300, 32, 20

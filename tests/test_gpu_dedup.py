@@ -72,6 +72,31 @@ def test_dedup_random(n, hi):
     check_against_oracle(keys)
 
 
+@pytest.mark.parametrize("case", ["below_bit_27", "bit_27_set_once", "high_common_bits", "int32_small",
+                                  "negative_mixed"])
+def test_dedup_sort_bits_first_assumed_then_checked(case):
+    """The sort first assumes the keys differ only below bit 27 (three 9-bit
+    passes, no host round trip) and checks the assumption against the key span
+    it reduces on the way; a batch that differs higher up is deduplicated
+    again on its exact bits.  Both sides of the boundary, keys sharing high
+    bits, and keys whose sign bit differs."""
+    rng = np.random.default_rng(27)
+    n = 70000
+    if case == "below_bit_27":
+        keys = rng.integers(0, 2**27, size=n).astype(np.int64)
+        keys[:2] = [0, 2**27 - 1]
+    elif case == "bit_27_set_once":
+        keys = rng.integers(0, 2**27, size=n).astype(np.int64)
+        keys[n // 2] = 2**27
+    elif case == "high_common_bits":
+        keys = (2**40 + 12345 + rng.integers(0, 2**26, size=n)).astype(np.int64)
+    elif case == "int32_small":
+        keys = rng.integers(0, 5_000_000, size=n).astype(np.int32)
+    else:
+        keys = rng.integers(-1000, 1000, size=n).astype(np.int64)
+    check_against_oracle(keys)
+
+
 def test_dedup_multi_level_scans():
     """4096 * 4096 + 3001 keys: the run-head scan recurses twice (more than
     4096 blocks of 4096) and each radix digit row spans several 1024-tile
