@@ -116,18 +116,17 @@ int64_t pooling_backprop_run(int key_bytes, int64_t n, const void* keys, int poo
   const void* csr = (!concat && sparse == NVE_SPARSE_CSR) ? offsets : nullptr;
   BackpropBufs b = carve(ws, n, num_bags);
 
-  // (1) dedup: unique keys straight into the caller's buffer
-  // (the unique count is read once everything is queued: no stall in between)
-  const DedupHead* head_dev = nullptr;
-  dedup_run(key_bytes, n, keys, unique_out, b.counts, b.inverse, b.doff, b.dedup_ws, b.dedup_bytes, s,
-            b.kidx, &head_dev, exact);
-
-  // (2) gradient row and weight per dedup position
+  // (1) bag denominators (Mean modes), then the dedup: unique keys straight
+  // into the caller's buffer, and (2) on the way the gradient row and weight
+  // of every dedup position (the unique count is read once everything is
+  // queued: no stall in between)
   if (mode == kBackpropMean || mode == kBackpropWMean)
     NVE_HIP(launch_bag_denom(csr, key_bytes, num_bags, hotness, weights, wdt, mode == kBackpropWMean,
                              b.denom, s));
-  NVE_HIP(launch_backprop_prep(b.inverse, key_bytes, n, mode, csr, num_bags, hotness, weights, wdt,
-                               b.denom, b.rows, b.nw, s));
+  const PositionGrad pg{mode, csr, key_bytes, num_bags, hotness, weights, wdt, b.denom, b.rows, b.nw};
+  const DedupHead* head_dev = nullptr;
+  dedup_run(key_bytes, n, keys, unique_out, b.counts, b.inverse, b.doff, b.dedup_ws, b.dedup_bytes, s,
+            b.kidx, &head_dev, exact, &pg);
 
   // (3) pieces, then the keys that cross a block edge
   PieceArgs a{};

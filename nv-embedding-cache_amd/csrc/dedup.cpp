@@ -4,6 +4,7 @@
 // 2^30 keys sort instead and gather in key order).
 #include "dedup.hpp"
 
+#include "kernels/backprop_launch.hpp"
 #include "kernels/cache_launch.hpp"
 #include "kernels/dedup_launch.hpp"
 #include "kernels/launch.hpp"
@@ -75,31 +76,33 @@ size_t dedup_workspace_bytes(int64_t n) {
 
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
                   void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
-                  uint32_t* pos_key, const DedupHead** head_dev, bool exact) {
+                  uint32_t* pos_key, const DedupHead** head_dev, bool exact, const PositionGrad* pg) {
   if (n <= 0) return 0;
   NVE_CHECK_ARG(n <= (int64_t)UINT32_MAX, "Too many keys for one dedup");
   NVE_CHECK_ARG(ws != nullptr && ws_bytes >= dedup_workspace_bytes(n), "Workspace too small");
   DedupBufs b = carve(ws, n);
-  int bits = kSpecSortBits;
+  // a single key needs no sort: it takes the exact path, which sorts nothing
+  if (n < 2) exact = true;
+  int alt = 0;
   if (exact) {
-    NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, nullptr, s));
+    NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, s));
     NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(&b.head->span), 1, 0, s));
     NVE_HIP(key_span(b.ka, n, &b.head->span, s));
-    bits = bits_for(read_back(&b.head->span, s));
+    const int bits = bits_for(read_back(&b.head->span, s));
+    NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, bits, b.sort_tmp, &alt, s));
   } else {
-    // the span is reduced on the way (prep's parts, outputs' workgroup 0) and
-    // checked by whoever reads the head
-    NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 1, b.ka, b.va, b.span_part, s));
+    // the first pass reads the caller's keys and writes each tile's span part;
+    // the outputs' workgroup 0 reduces them and whoever reads the head checks
+    const RadixSource src{keys, key_bytes, 1, b.span_part};
+    NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, kSpecSortBits, b.sort_tmp, &alt, s, &src));
   }
-  int alt = 0;
-  NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0, bits, b.sort_tmp, &alt, s));
   const uint64_t* ks = alt ? b.kb : b.ka;
   const uint32_t* vs = alt ? b.vb : b.va;
   if (run_blocks(n) <= kRunMaxBlocks) {
     // every output in two launches (block scratch in the heads / start arrays)
     NVE_HIP(launch_dedup_runs(ks, vs, n, key_bytes, unique, counts, inverse, offsets, pos_key, &b.head->total,
                               b.heads, reinterpret_cast<int64_t*>(b.start), exact ? nullptr : b.span_part,
-                              exact ? nullptr : &b.head->span, s));
+                              exact ? nullptr : &b.head->span, pg, s));
     if (head_dev != nullptr) {
       *head_dev = b.head;
       return -1;
@@ -107,13 +110,14 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
     const DedupHead h = read_back(b.head, s);
     if (!exact && dedup_spec_failed(h))
       return dedup_run(key_bytes, n, keys, unique, counts, inverse, offsets, ws, ws_bytes, s, pos_key, nullptr,
-                       true);
+                       true, pg);
     return (int64_t)h.total;
   }
   NVE_HIP(launch_run_heads(ks, n, b.heads, s));
   NVE_HIP(exclusive_scan_u32(b.heads, n, &b.head->total, b.sort_tmp, s));
   NVE_HIP(launch_dedup_outputs(ks, vs, b.heads, n, key_bytes, unique, inverse, offsets, b.start, pos_key,
                                exact ? nullptr : b.span_part, exact ? nullptr : &b.head->span, s));
+  if (pg != nullptr) NVE_HIP(launch_backprop_prep(inverse, key_bytes, n, *pg, s));
   if (head_dev != nullptr) {  // the caller reads the head when it needs it
     NVE_HIP(launch_dedup_counts(b.start, (uint32_t)n, &b.head->total, key_bytes, counts, s));
     *head_dev = b.head;
@@ -122,7 +126,7 @@ int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void
   const DedupHead h = read_back(b.head, s);
   if (!exact && dedup_spec_failed(h))
     return dedup_run(key_bytes, n, keys, unique, counts, inverse, offsets, ws, ws_bytes, s, pos_key, nullptr,
-                     true);
+                     true, pg);
   NVE_HIP(launch_dedup_counts(b.start, h.total, nullptr, key_bytes, counts, s));
   return (int64_t)h.total;
 }
@@ -153,7 +157,7 @@ void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t*
   DedupBufs b = carve(ws, n);
   // rows of [0, num_rows): sort on the row-index bits only (keys outside the
   // table stay unresolved and their output rows untouched)
-  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, nullptr, s));
+  NVE_HIP(launch_dedup_prep(keys, key_bytes, n, 0, b.ka, b.va, s));
   int alt = 0;
   NVE_HIP(radix_sort_pairs(b.ka, b.va, b.kb, b.vb, n, 0,
                            bits_for((uint64_t)(num_rows > 1 ? num_rows - 1 : 1)),

@@ -6,6 +6,8 @@
 
 #include <cstddef>
 
+#include "kernels/backprop_launch.hpp"
+
 namespace nve_amd {
 
 size_t dedup_workspace_bytes(int64_t n);
@@ -35,9 +37,12 @@ inline bool dedup_spec_failed(const DedupHead& h) { return (h.span >> kSpecSortB
 // reused); the caller reads it and, if dedup_spec_failed, runs again with
 // exact = true.  exact: read the key span back first and sort on exactly its
 // bits (never needs a second run).
+// pg (optional): also each dedup position's gradient row and weight (the
+// backprop's per-position step, done on the way).
 int64_t dedup_run(int key_bytes, int64_t n, const void* keys, void* unique, void* counts,
                   void* inverse, void* offsets, void* ws, size_t ws_bytes, hipStream_t s,
-                  uint32_t* pos_key = nullptr, const DedupHead** head_dev = nullptr, bool exact = false);
+                  uint32_t* pos_key = nullptr, const DedupHead** head_dev = nullptr, bool exact = false,
+                  const PositionGrad* pg = nullptr);
 
 // out[i] = table row keys[i] for keys in [0, num_rows), each distinct row read
 // from the table once (asynchronous).

@@ -22,6 +22,7 @@
 #include "backprop_launch.hpp"
 #include "device_common.cuh"
 #include "lane_moves.cuh"
+#include "position_grad.cuh"
 
 namespace nve_amd {
 
@@ -57,46 +58,11 @@ __global__ __launch_bounds__(256) void bag_denom_kernel(const void* offsets, int
   denom[b] = acc;
 }
 
-// bag holding position p, or -1 (Fixed: p / hotness; CSR: binary search for
-// the last b with offsets[b] <= p, valid when p < offsets[b + 1])
-__device__ __forceinline__ int64_t bag_of(int64_t p, const void* offsets, int key_bytes,
-                                          int64_t num_bags, int64_t hotness) {
-  if (offsets == nullptr) {
-    const int64_t b = hotness > 0 ? p / hotness : -1;
-    return (b >= 0 && b < num_bags) ? b : -1;
-  }
-  if (num_bags <= 0 || load_key(offsets, key_bytes, 0) > p) return -1;
-  int64_t lo = 0, hi = num_bags;
-  while (hi - lo > 1) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (load_key(offsets, key_bytes, mid) <= p) lo = mid;
-    else hi = mid;
-  }
-  return p < load_key(offsets, key_bytes, lo + 1) ? lo : -1;
-}
-
-// For dedup position j (key position p = inverse[j]): the gradient row it
-// reads (Concatenate: p; pooled: its bag, or none_row outside every bag) and
-// its weight (1, w[p], 1 / count or w[p] / sum of the bag's weights).
-__global__ __launch_bounds__(256) void backprop_prep_kernel(
-    const void* inverse, int key_bytes, int64_t n, int mode, const void* offsets, int64_t num_bags,
-    int64_t hotness, const void* weights, int wdt, const float* denom, uint32_t* rows, float* nw) {
+// rows / nw of dedup position j (key position p = inverse[j])
+__global__ __launch_bounds__(256) void backprop_prep_kernel(const void* inverse, int key_bytes, int64_t n,
+                                                            PositionGrad g) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const int64_t p = load_key(inverse, key_bytes, j);
-  uint32_t row = (uint32_t)p;
-  float w = 1.0f;
-  if (mode != kBackpropConcat) {
-    const int64_t b = bag_of(p, offsets, key_bytes, num_bags, hotness);
-    row = b < 0 ? kNoGradRow : (uint32_t)b;
-    if (b >= 0) {
-      if (mode == kBackpropWSum) w = load_weight(weights, wdt, p);
-      else if (mode == kBackpropMean) w = 1.0f / denom[b];
-      else if (mode == kBackpropWMean) w = load_weight(weights, wdt, p) / denom[b];
-    }
-  }
-  rows[j] = row;
-  nw[j] = w;
+  if (j < n) position_grad(g, j, load_key(inverse, key_bytes, j));
 }
 
 constexpr int kPieceThreads = 256;
@@ -389,14 +355,11 @@ hipError_t launch_bag_denom(const void* offsets, int key_bytes, int64_t num_bags
   return hipGetLastError();
 }
 
-hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, int mode,
-                                const void* offsets, int64_t num_bags, int64_t hotness,
-                                const void* weights, int wdt, const float* denom, uint32_t* rows,
-                                float* nw, hipStream_t stream) {
+hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, const PositionGrad& g,
+                                hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(backprop_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     inverse, key_bytes, n, mode, offsets, num_bags, hotness, weights, wdt, denom,
-                     rows, nw);
+                     inverse, key_bytes, n, g);
   return hipGetLastError();
 }
 

@@ -22,10 +22,25 @@ constexpr int kPieceFanIn = 8;
 constexpr int kCombineBlocks = 8;  // block entries per combine workgroup
 constexpr int kLightPieces = 32;   // a crossing key of more pieces is added by a whole workgroup
 
-hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, int mode,
-                                const void* offsets, int64_t num_bags, int64_t hotness,
-                                const void* weights, int wdt, const float* denom, uint32_t* rows,
-                                float* nw, hipStream_t stream);
+// What the backprop needs per key position: how its gradient row and weight
+// follow from its position (the bags, weights and bag denominators), and
+// where they go (rows / nw, one entry per dedup position; rows null: none).
+struct PositionGrad {
+  int mode;             // kBackprop*
+  const void* offsets;  // CSR offsets of the key type, or null (Fixed hotness)
+  int key_bytes;
+  int64_t num_bags;
+  int64_t hotness;
+  const void* weights;
+  int wdt;
+  const float* denom;   // Mean / WeightedMean: per bag
+  uint32_t* rows;
+  float* nw;
+};
+
+// rows / nw of every dedup position j from inverse[j] (its key position).
+hipError_t launch_backprop_prep(const void* inverse, int key_bytes, int64_t n, const PositionGrad& g,
+                                hipStream_t stream);
 
 struct PieceArgs {
   const uint32_t* kidx;  // unique index of each dedup position

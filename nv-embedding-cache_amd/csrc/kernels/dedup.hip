@@ -18,6 +18,8 @@
 // cuda_utils.cuh:24-79).
 #include "device_common.cuh"
 #include "dedup_launch.hpp"
+#include "position_grad.cuh"
+#include "sort_launch.hpp"
 
 namespace nve_amd {
 
@@ -31,26 +33,13 @@ __device__ __forceinline__ uint64_t block_or(uint64_t x) {
   return red[0] | red[1] | red[2] | red[3];
 }
 
-// span_part (optional): span_part[b] = OR over workgroup b's keys of
-// key ^ key[0] (sort keys), the bits where they differ from the first key.
 __global__ __launch_bounds__(256) void dedup_prep_kernel(const void* keys, int key_bytes, int64_t n,
-                                                         int flip, uint64_t* k64, uint32_t* v,
-                                                         uint64_t* span_part) {
+                                                         int flip, uint64_t* k64, uint32_t* v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  uint64_t diff = 0;
   if (i < n) {
     const int64_t k = load_key(keys, key_bytes, i);
-    const uint64_t kk = flip ? flip_key(k, key_bytes) : (uint64_t)k;
-    k64[i] = kk;
+    k64[i] = flip ? flip_key(k, key_bytes) : (uint64_t)k;
     v[i] = (uint32_t)i;
-    if (span_part != nullptr) {
-      const int64_t k0 = load_key(keys, key_bytes, 0);
-      diff = kk ^ (flip ? flip_key(k0, key_bytes) : (uint64_t)k0);
-    }
-  }
-  if (span_part != nullptr) {  // uniform: the whole workgroup reduces
-    const uint64_t d = block_or(diff);
-    if (threadIdx.x == 0) span_part[blockIdx.x] = d;
   }
 }
 
@@ -190,6 +179,7 @@ struct RunOutputs {
   const uint64_t* span_part;  // optional: block 0 ORs these into *span_out
   int64_t nparts;
   unsigned long long* span_out;
+  PositionGrad pg;            // pg.rows non-null: each position's gradient row and weight too
 };
 
 __global__ __launch_bounds__(kRunThreads) void run_outputs_kernel(RunOutputs a) {
@@ -268,8 +258,10 @@ __global__ __launch_bounds__(kRunThreads) void run_outputs_kernel(RunOutputs a) 
       store_key(a.unique, a.key_bytes, u, unflip_key(k[j], a.key_bytes));
       store_key(a.offsets, a.key_bytes, u, i);
     }
-    store_key(a.inverse, a.key_bytes, i, (int64_t)a.vs[i]);
+    const uint32_t pos = a.vs[i];
+    store_key(a.inverse, a.key_bytes, i, (int64_t)pos);
     if (a.pos_key != nullptr) a.pos_key[i] = u;
+    if (a.pg.rows != nullptr) position_grad(a.pg, i, (int64_t)pos);
     const bool tail = i == a.n - 1 || k[j] != (j + 1 < kRunItems ? k[j + 1] : after);
     if (tail) store_key(a.counts, a.key_bytes, u, i + 1 - start);
   }
@@ -553,13 +545,13 @@ hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, 
   return hipGetLastError();
 }
 
-int64_t dedup_span_parts(int64_t n) { return n > 0 ? (n + 255) / 256 : 0; }
+int64_t dedup_span_parts(int64_t n) { return radix_tiles(n); }
 
 hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int flip, uint64_t* k64,
-                             uint32_t* v, uint64_t* span_part, hipStream_t stream) {
+                             uint32_t* v, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(dedup_prep_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, keys, key_bytes,
-                     n, flip, k64, v, span_part);
+                     n, flip, k64, v);
   return hipGetLastError();
 }
 
@@ -580,13 +572,13 @@ int64_t run_blocks(int64_t n) { return (n + kRunBlock - 1) / kRunBlock; }
 hipError_t launch_dedup_runs(const uint64_t* ks, const uint32_t* vs, int64_t n, int key_bytes, void* unique,
                              void* counts, void* inverse, void* offsets, uint32_t* pos_key, uint32_t* total,
                              uint32_t* blk_count, int64_t* blk_last, const uint64_t* span_part,
-                             unsigned long long* span_out, hipStream_t stream) {
+                             unsigned long long* span_out, const PositionGrad* pg, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const int64_t nb = run_blocks(n);
   if (nb > kRunMaxBlocks) return hipErrorInvalidValue;
   hipLaunchKernelGGL(run_block_kernel, dim3(nb), dim3(kRunThreads), 0, stream, ks, n, blk_count, blk_last);
   RunOutputs a{ks, vs, n, blk_count, blk_last, key_bytes, unique, counts, inverse, offsets, pos_key, total,
-               span_part, dedup_span_parts(n), span_out};
+               span_part, dedup_span_parts(n), span_out, pg != nullptr ? *pg : PositionGrad{}};
   hipLaunchKernelGGL(run_outputs_kernel, dim3(nb), dim3(kRunThreads), 0, stream, a);
   return hipGetLastError();
 }

@@ -4,16 +4,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "backprop_launch.hpp"
+
 namespace nve_amd {
 
-// Words of the prep's per-workgroup key-span parts for n keys.
+// Words of the key-span parts the radix sort's first pass writes for n keys
+// (one per tile, radix_tiles(n)).
 int64_t dedup_span_parts(int64_t n);
-// k64[i] = key i as an unsigned sort key (sign bit flipped when flip != 0), v[i] = i;
-// span_part (optional, dedup_span_parts(n) words): per-workgroup OR of k64[i] ^ k64[0].
+// k64[i] = key i as an unsigned sort key (sign bit flipped when flip != 0), v[i] = i.
 hipError_t launch_dedup_prep(const void* keys, int key_bytes, int64_t n, int flip, uint64_t* k64,
-                             uint32_t* v, uint64_t* span_part, hipStream_t stream);
-// Outputs from the sorted keys and the run-head scan; with span_part, also
-// *span_out = OR of the prep's span parts.
+                             uint32_t* v, hipStream_t stream);
+// Outputs from the sorted keys and the run-head scan; with span_part
+// (dedup_span_parts(n) words), also *span_out = OR of the span parts.
 hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan,
                                 int64_t n, int key_bytes, void* unique, void* inverse,
                                 void* offsets, uint32_t* start, uint32_t* pos_key,
@@ -22,14 +24,16 @@ hipError_t launch_dedup_outputs(const uint64_t* ks, const uint32_t* vs, const ui
 // The runs of sorted keys ks (values vs) in two launches: unique keys, counts,
 // inverse and offsets of the key type, pos_key (optional) the unique index of
 // every position, *total the unique count; with span_part, also *span_out as
-// launch_dedup_outputs.  Scratch: blk_count / blk_last, run_blocks(n) words
-// each.  At most kRunMaxBlocks blocks (hipErrorInvalidValue beyond).
+// launch_dedup_outputs; with pg, each dedup position's gradient row and
+// weight (as launch_backprop_prep).  Scratch: blk_count / blk_last,
+// run_blocks(n) words each.  At most kRunMaxBlocks blocks
+// (hipErrorInvalidValue beyond).
 constexpr int64_t kRunMaxBlocks = 4096;
 int64_t run_blocks(int64_t n);
 hipError_t launch_dedup_runs(const uint64_t* ks, const uint32_t* vs, int64_t n, int key_bytes, void* unique,
                              void* counts, void* inverse, void* offsets, uint32_t* pos_key, uint32_t* total,
                              uint32_t* blk_count, int64_t* blk_last, const uint64_t* span_part,
-                             unsigned long long* span_out, hipStream_t stream);
+                             unsigned long long* span_out, const PositionGrad* pg, hipStream_t stream);
 // counts[u] for u < u_n, or for u < *u_dev when u_dev is given (u_n an upper bound).
 hipError_t launch_dedup_counts(const uint32_t* start, uint32_t u_n, const uint32_t* u_dev,
                                int key_bytes, void* counts, hipStream_t stream);

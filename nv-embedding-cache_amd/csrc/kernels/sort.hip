@@ -38,9 +38,24 @@ constexpr int kSortItems = 4;
 constexpr int kSortTile = kSortThreads * kSortItems;
 constexpr int kMaxBins = 512;  // digits of at most 9 bits
 
-template <int RB>
-__global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, int64_t n, int shift,
-                                                         uint32_t mask, uint32_t* counts, int nblocks) {
+// The sort key of position i: keys[i], or with a raw source the caller's key
+// converted on the fly (sign bit flipped when src.flip).
+template <bool RAW>
+__device__ __forceinline__ uint64_t sort_key(const uint64_t* keys, const RadixSource& src, int64_t i) {
+  if constexpr (RAW) {
+    const int64_t k = load_key(src.keys, src.key_bytes, i);
+    return src.flip ? flip_key(k, src.key_bytes) : (uint64_t)k;
+  } else {
+    return keys[i];
+  }
+}
+
+// RAW: the first pass over the caller's keys; with src.span_part, also the
+// tile's OR of key ^ key[0] (the bits where its keys differ from the first).
+template <int RB, bool RAW>
+__global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, RadixSource src, int64_t n,
+                                                         int shift, uint32_t mask, uint32_t* counts,
+                                                         int nblocks) {
   constexpr int kBins = 1 << RB;
   __shared__ uint32_t h[kBins];
   const int tid = threadIdx.x;
@@ -48,10 +63,31 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint64_t* keys, i
   for (int d = tid; d < kBins; d += kSortThreads) h[d] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  uint64_t diff = 0;
+  const uint64_t k0 = RAW && src.span_part != nullptr ? sort_key<RAW>(keys, src, 0) : 0;
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t i = base + r * kSortThreads + tid;
-    if (i < n) atomicAdd(&h[(uint32_t)(keys[i] >> shift) & mask], 1u);
+    if (i < n) {
+      const uint64_t k = sort_key<RAW>(keys, src, i);
+      atomicAdd(&h[(uint32_t)(k >> shift) & mask], 1u);
+      diff |= k ^ k0;
+    }
+  }
+  if constexpr (RAW) {
+    if (src.span_part != nullptr) {  // uniform
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) diff |= __shfl_xor(diff, o);
+      __shared__ uint64_t red[kSortThreads / 64];
+      if ((tid & 63) == 0) red[tid >> 6] = diff;
+      __syncthreads();
+      if (tid == 0) {
+        uint64_t x = 0;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / 64; ++w) x |= red[w];
+        src.span_part[blockIdx.x] = x;
+      }
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -184,10 +220,12 @@ __global__ __launch_bounds__(256) void radix_rowscan_kernel(const uint32_t* coun
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
-template <int RB>
+// RAW: the first pass reads the caller's keys (src) and takes each key's
+// position as its value.
+template <int RB, bool RAW>
 __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys, const uint32_t* vals,
-                                                            uint64_t* ko, uint32_t* vo, int64_t n,
-                                                            int shift, uint32_t mask,
+                                                            RadixSource src, uint64_t* ko, uint32_t* vo,
+                                                            int64_t n, int shift, uint32_t mask,
                                                             const uint32_t* counts,
                                                             const uint32_t* offs,
                                                             const uint32_t* totals, int nblocks) {
@@ -211,8 +249,11 @@ __global__ __launch_bounds__(256) void radix_scatter_kernel(const uint64_t* keys
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int li = r * kSortThreads + tid;
-    k[r] = li < tile_n ? keys[base + li] : 0ull;
-    v[r] = li < tile_n ? vals[base + li] : 0u;
+    k[r] = li < tile_n ? sort_key<RAW>(keys, src, base + li) : 0ull;
+    if constexpr (RAW)
+      v[r] = (uint32_t)(base + li);
+    else
+      v[r] = li < tile_n ? vals[base + li] : 0u;
   }
   // thread t owns digits t*D .. t*D+D-1
   uint32_t dbase[D], loc[D];
@@ -325,9 +366,9 @@ size_t radix_sort_temp_bytes(int64_t n) {
 
 hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, uint32_t* vals_alt,
                             int64_t n, int begin_bit, int end_bit, void* temp, int* result_in_alt,
-                            hipStream_t stream) {
+                            hipStream_t stream, const RadixSource* src) {
   *result_in_alt = 0;
-  if (n <= 1 || end_bit <= begin_bit) return hipSuccess;
+  if (n <= 1 || end_bit <= begin_bit) return src != nullptr ? hipErrorInvalidValue : hipSuccess;
   const int64_t nblocks = (n + kSortTile - 1) / kSortTile;
   if (nblocks > 0x7fffffff) return hipErrorInvalidValue;
   uint32_t* counts = static_cast<uint32_t*>(temp);
@@ -337,6 +378,7 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   uint32_t* vi = vals;
   uint64_t* ka = keys_alt;
   uint32_t* va = vals_alt;
+  const RadixSource none{};
   // 9-bit digits when they take fewer passes than 8-bit ones (26-bit keys: 3
   // passes instead of 4); the last digit keeps only the bits below end_bit
   const int width = end_bit - begin_bit;
@@ -344,27 +386,37 @@ hipError_t radix_sort_pairs(uint64_t* keys, uint32_t* vals, uint64_t* keys_alt, 
   for (int shift = begin_bit; shift < end_bit; shift += rb) {
     const int bits = end_bit - shift < rb ? end_bit - shift : rb;
     const uint32_t mask = (1u << bits) - 1u;
+    const bool raw = src != nullptr && shift == begin_bit;
+    const RadixSource& s = raw ? *src : none;
+#define NVE_RADIX_PASS(RB, RAW)                                                                           \
+  hipLaunchKernelGGL((radix_hist_kernel<RB, RAW>), dim3(nblocks), dim3(kSortThreads), 0, stream, ki, s, n, \
+                     shift, mask, counts, (int)nblocks);                                                  \
+  hipLaunchKernelGGL(radix_rowscan_kernel, dim3(1u << RB), dim3(256), 0, stream, counts, offs,            \
+                     (int)nblocks, totals);                                                               \
+  hipLaunchKernelGGL((radix_scatter_kernel<RB, RAW>), dim3(nblocks), dim3(kSortThreads), 0, stream, ki,   \
+                     vi, s, ka, va, n, shift, mask, counts, offs, totals, (int)nblocks)
     if (rb == 9) {
-      hipLaunchKernelGGL(radix_hist_kernel<9>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
-                         shift, mask, counts, (int)nblocks);
-      hipLaunchKernelGGL(radix_rowscan_kernel, dim3(1u << 9), dim3(256), 0, stream, counts, offs,
-                         (int)nblocks, totals);
-      hipLaunchKernelGGL(radix_scatter_kernel<9>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki,
-                         vi, ka, va, n, shift, mask, counts, offs, totals, (int)nblocks);
+      if (raw) {
+        NVE_RADIX_PASS(9, true);
+      } else {
+        NVE_RADIX_PASS(9, false);
+      }
     } else {
-      hipLaunchKernelGGL(radix_hist_kernel<8>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki, n,
-                         shift, mask, counts, (int)nblocks);
-      hipLaunchKernelGGL(radix_rowscan_kernel, dim3(1u << 8), dim3(256), 0, stream, counts, offs,
-                         (int)nblocks, totals);
-      hipLaunchKernelGGL(radix_scatter_kernel<8>, dim3(nblocks), dim3(kSortThreads), 0, stream, ki,
-                         vi, ka, va, n, shift, mask, counts, offs, totals, (int)nblocks);
+      if (raw) {
+        NVE_RADIX_PASS(8, true);
+      } else {
+        NVE_RADIX_PASS(8, false);
+      }
     }
+#undef NVE_RADIX_PASS
     std::swap(ki, ka);
     std::swap(vi, va);
     *result_in_alt ^= 1;
   }
   return hipGetLastError();
 }
+
+int64_t radix_tiles(int64_t n) { return n > 0 ? (n + kSortTile - 1) / kSortTile : 0; }
 
 hipError_t exclusive_scan_u32(uint32_t* data, int64_t m, uint32_t* total, void* temp,
                               hipStream_t stream) {
