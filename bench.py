@@ -696,7 +696,7 @@ def run_workload(args, torch, _lib):
         cfg_out.update({"table_rows": rows, "dim": dim, "bags": bags, "hotness": hot, "zipf_alpha": alpha,
                         "keys_per_batch": nkeys, "mean_unique_keys": u, "pooling": "sum",
                         "grad_dtype": "f16", "step": "one nve_amd_pooling_backprop call (synchronizes)"})
-        kernel = "radix dedup + backprop_prep + piece_pool_kernel + piece_combine_kernel"
+        kernel = "radix dedup (first pass on the raw keys; runs and per-position rows in two launches) + piece_pool_kernel + piece_combine_kernel"
     elif w == "c5":
         T, B, dim = 26, 8192, 128
         cg = torch.Generator()
