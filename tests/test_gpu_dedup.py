@@ -97,6 +97,22 @@ def test_dedup_sort_bits_first_assumed_then_checked(case):
     check_against_oracle(keys)
 
 
+@pytest.mark.parametrize("n", [2, 3, 1023, 1024, 1025, 4096 * 1024, 4096 * 1024 + 1])
+@pytest.mark.parametrize("distinct", [1, 7, None])
+def test_dedup_run_block_edges(n, distinct):
+    """The runs are written by 1024-key blocks that take the head counts and
+    last heads of the blocks before them as carry-in, for up to 4096 blocks
+    (one more block falls back to the scan-based path): sizes on either side
+    of a block and of that limit, with one key (a single run through every
+    block), seven keys (runs crossing block edges) and all-distinct keys."""
+    rng = np.random.default_rng(n + (distinct or 0))
+    if distinct is None:
+        keys = rng.permutation(n).astype(np.int64)
+    else:
+        keys = rng.integers(0, distinct, size=n).astype(np.int64) * 1000003
+    check_against_oracle(keys)
+
+
 def test_dedup_multi_level_scans():
     """4096 * 4096 + 3001 keys: the run-head scan recurses twice (more than
     4096 blocks of 4096) and each radix digit row spans several 1024-tile
