@@ -639,6 +639,27 @@ def run_workload(args, torch, _lib):
         hit = sum(rates) / len(rates)
         log(f"c3: {ms * 1000:.1f} us/step (events), {wall * 1000:.1f} us/step (wall), mean hit rate {hit:.4f}")
         ms = max(ms, wall)  # the step includes a host sync (hit rate) and any insert
+        if args.c3_insert_steps > 0 and not args.c3_prefill:
+            # the insert behind auto-insert, timed on its own: histogram of a whole
+            # batch, replacement, rows copied from the host table (the reference's
+            # GpuTable::insert path, gpu_table.cu:579-1046), each call waited for
+            tctx = ctypes.c_void_p()
+            _lib.call("nve_table_create_execution_context", table, ctypes.byref(tctx), sp, sp, None, None)
+            ins = []
+            for i in range(args.c3_insert_steps + 1):
+                b = batches[(10 + nt + i) % len(batches)]
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                _lib.call("nve_amd_table_insert_from_uvm", table, tctx, nkeys, ctypes.c_void_p(b.data_ptr()))
+                _lib.call("nve_context_wait", tctx)
+                torch.cuda.synchronize()
+                if i:  # the first call sizes its scratch
+                    ins.append((time.perf_counter() - t0) * 1e6)
+            _lib.call("nve_context_destroy", tctx)
+            ins.sort()
+            cfg_out["insert_us"] = {"median": round(ins[len(ins) // 2], 1), "min": round(ins[0], 1),
+                                    "max": round(ins[-1], 1), "calls": len(ins), "keys_per_call": nkeys}
+            log(f"c3: insert of a {nkeys}-key batch: median {ins[len(ins) // 2]:.1f} us over {len(ins)} calls")
         # HBM: keys + 8 tags (64 B) per key + cached rows; host link: missed rows
         alg = (nkeys * (8 + 64) + int(nkeys * hit) * width + int(nkeys * (1 - hit)) * width
                + (nkeys if concat else bags) * width)
@@ -808,6 +829,8 @@ def main():
                     help="c3: keys per batch (a multiple of --c3-hotness)")
     ap.add_argument("--c3-no-touch", action="store_true",
                     help="c3: leave the DMA-filled host table's pages unmapped on the host")
+    ap.add_argument("--c3-insert-steps", type=int, default=5,
+                    help="c3: time this many whole-batch inserts from the backing table after the lookups")
     ap.add_argument("--c3-prefill", action="store_true",
                     help="c3: insert every backing row into the cache before the lookups (hit path only)")
     ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],
