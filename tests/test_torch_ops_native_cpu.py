@@ -73,3 +73,56 @@ def test_op_lookups_log_hit_rates_at_perf_level():
     lines = [s for s in p.stdout.splitlines() if "Hit rates:" in s]
     assert len(lines) == 2 and all("][P] Hit rates: " in s for s in lines), p.stdout  # lookups 0 and 2 of 3
     assert "OK" in p.stdout
+
+
+def _host_bag():
+    from pynve.torch import nve_layers
+    init = torch.arange(40 * 4, dtype=torch.float32).reshape(40, 4)
+    return nve_layers.NVEmbeddingBag(40, 4, torch.float32, nve_layers.LayerType.HostLayer, "sum",
+                                     weight_init=init, optimize_for_training=False, device="cpu"), init
+
+
+def test_op_checks_and_status_mapping():
+    """The C++ ops check their tensors (nve_torch_ops_checks.hpp:27-45 in the
+    reference) and map the C ABI's status to Python exceptions: an invalid
+    argument is a ValueError, any other failure a RuntimeError."""
+    bag, init = _host_bag()
+    m = bag.marker_tensor
+    keys = torch.tensor([1, 2, 3, 39], dtype=torch.int64)
+    off = torch.tensor([0, 2, 4], dtype=torch.int64)
+    op = torch.ops.nve_ops.embedding_lookup_with_pooling
+    out = op(m, keys, off, None, 1, 4, 1)
+    assert torch.equal(out, torch.stack([init[1] + init[2], init[3] + init[39]]))
+    with pytest.raises(RuntimeError, match="int64"):
+        op(m, keys.int(), off, None, 1, 4, 1)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        op(m, torch.arange(8, dtype=torch.int64)[::2], off, None, 1, 4, 1)
+    with pytest.raises(RuntimeError, match="num_bags"):
+        op(m, keys, off[:1], None, 1, 4, 1)
+    with pytest.raises(RuntimeError, match="float32 or float16"):
+        op(m, keys, off, torch.ones(4, dtype=torch.float64), 3, 4, 1)
+    with pytest.raises(RuntimeError, match="one per key"):
+        op(m, keys, off, torch.ones(3), 3, 4, 1)
+    with pytest.raises(ValueError, match="invalid argument"):  # the C ABI rejects the pooling type
+        op(m, keys, off, None, 77, 4, 1)
+    # weighted sum through the op, weights of the table's dtype
+    w = torch.tensor([1.0, 0.5, 2.0, 0.25])
+    out = op(m, keys, off, w, 3, 4, 1)
+    assert torch.equal(out, torch.stack([init[1] + 0.5 * init[2], 2.0 * init[3] + 0.25 * init[39]]))
+    rows = torch.ops.nve_ops.embedding_lookup(m, keys, 4, 1)
+    assert torch.equal(rows, init[keys])
+
+
+def test_unregistered_marker_after_the_layer_is_gone():
+    import gc
+    bag, _ = _host_bag()
+    m = bag.marker_tensor
+    keys = torch.tensor([1], dtype=torch.int64)
+    assert torch.ops.nve_ops.embedding_lookup(m, keys, 4, 1).shape == (1, 4)
+    marker_copy = m.clone()  # a tensor at another address was never registered
+    with pytest.raises(RuntimeError, match="no binding registered"):
+        torch.ops.nve_ops.embedding_lookup(marker_copy, keys, 4, 1)
+    del bag
+    gc.collect()
+    with pytest.raises(RuntimeError, match="no binding registered"):
+        torch.ops.nve_ops.embedding_lookup(m, keys, 4, 1)
