@@ -60,6 +60,25 @@ hipError_t launch_fill_u64(uint64_t* p, int64_t count, uint64_t v, hipStream_t s
   return hipGetLastError();
 }
 
+// *total = the sum of the counter's words, stored straight into pinned host
+// memory (no copy operation behind the kernel); with reset, the words
+// become 0 for the next count.
+__global__ __launch_bounds__(64) void counter_total_kernel(unsigned long long* words, int n,
+                                                           unsigned long long* total, int reset) {
+  if (threadIdx.x != 0) return;
+  unsigned long long t = 0;
+  for (int i = 0; i < n; ++i) t += words[i];
+  if (reset)
+    for (int i = 0; i < n; ++i) words[i] = 0;
+  *total = t;
+}
+
+hipError_t launch_counter_total(unsigned long long* words, int n, unsigned long long* host_total, int reset,
+                                hipStream_t stream) {
+  hipLaunchKernelGGL(counter_total_kernel, dim3(1), dim3(64), 0, stream, words, n, host_total, reset);
+  return hipGetLastError();
+}
+
 hipError_t launch_cache_erase(void* tags, const void* keys, int64_t n, int key_bytes,
                               uint64_t num_sets, int64_t sentinel, hipStream_t stream) {
   if (n <= 0) return hipSuccess;

@@ -203,6 +203,7 @@ ExecutionContext::~ExecutionContext() {
       (void)hipFree(kv.second.ptr);
   }
   if (misses_) (void)hipFree(misses_);
+  if (miss_total_) (void)hipHostFree(miss_total_);
 }
 
 void* ExecutionContext::host_buffer(const std::string& name, size_t bytes) {
@@ -255,16 +256,34 @@ unsigned long long* ExecutionContext::miss_counter() {
     NVE_HIP(hipMalloc(&misses_, kMissCounterWords * sizeof(unsigned long long)));
     NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(misses_), kMissCounterWords, 0, lookup_));
   }
+  misses_clean_ = false;  // the caller may hand it to a counting kernel
   return misses_;
 }
 
 void ExecutionContext::reset_misses() {
   // a fill kernel rather than a memset node, so the lookup stays capturable
   NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(miss_counter()), kMissCounterWords, 0, lookup_));
+  misses_clean_ = true;
 }
 
-int64_t ExecutionContext::read_misses() {
-  return read_miss_words(miss_counter(), lookup_);
+void ExecutionContext::prepare_misses() {
+  if (!misses_clean_) reset_misses();
+}
+
+int64_t ExecutionContext::misses_total(int reset) {
+  if (!misses_) miss_counter();
+  if (!miss_total_) NVE_HIP(hipHostMalloc((void**)&miss_total_, 64, hipHostMallocDefault));
+  NVE_HIP(launch_counter_total(misses_, kMissCounterWords, miss_total_, reset, lookup_));
+  NVE_HIP(hipStreamSynchronize(lookup_));
+  return (int64_t)*static_cast<volatile unsigned long long*>(miss_total_);
+}
+
+int64_t ExecutionContext::read_misses() { return misses_total(0); }
+
+int64_t ExecutionContext::take_misses() {
+  const int64_t t = misses_total(1);
+  misses_clean_ = true;
+  return t;
 }
 
 int64_t read_miss_words(const unsigned long long* counter, hipStream_t stream) {

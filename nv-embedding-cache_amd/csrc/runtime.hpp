@@ -170,9 +170,15 @@ class ExecutionContext {
   void watch(const std::shared_ptr<LookupStreams>& streams);
 
   // Device counter of cache misses (zeroed by reset_misses on lookup_stream).
+  // Asking for it marks it as possibly counting; read_misses returns its total
+  // (a kernel writes it into pinned host memory, then lookup_stream is
+  // synchronized), take_misses does the same and zeroes the counter, and
+  // prepare_misses zeroes it only when something may have counted since.
   unsigned long long* miss_counter();
   void reset_misses();
-  int64_t read_misses();  // syncs lookup_stream
+  int64_t read_misses();
+  int64_t take_misses();
+  void prepare_misses();
 
   void add_pending(std::future<void> f);
   void wait();
@@ -190,6 +196,9 @@ class ExecutionContext {
   std::mutex bufs_mu_;  // the lookup thread and a pool task (auto-insert) share buffers
   std::map<std::string, Buf> bufs_;
   unsigned long long* misses_ = nullptr;
+  unsigned long long* miss_total_ = nullptr;  // pinned host word the total is written to
+  bool misses_clean_ = false;                  // the counter is zero on lookup_stream
+  int64_t misses_total(int reset);
   int64_t host_counter_ = 0;
   std::mutex pending_mu_;
   std::vector<std::future<void>> pending_;

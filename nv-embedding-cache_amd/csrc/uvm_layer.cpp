@@ -79,7 +79,7 @@ void LinearUVMEmbeddingLayer::lookup(ExecutionContext& ctx, int64_t num_keys, co
   const bool collect = hitrates != nullptr || !never;
   if (collect) {
     NVE_CHECK(tc.count_misses, "GPU table was not configured to report hit counts");
-    ctx.reset_misses();
+    ctx.prepare_misses();
   }
   void* d_out = device_output(ctx, "output", output, out_bytes);
   if (pooled) {
@@ -98,7 +98,7 @@ void LinearUVMEmbeddingLayer::lookup(ExecutionContext& ctx, int64_t num_keys, co
   }
   finish_output(output, d_out, out_bytes, stream);
   if (collect) {
-    const int64_t misses = ctx.read_misses();  // syncs the lookup stream
+    const int64_t misses = ctx.take_misses();  // syncs the lookup stream, leaves the counter at 0
     const float hitrate =
         num_keys > 0 ? 1.0f - (float)misses / (float)num_keys : 1.0f;
     if (hitrates) *hitrates = hitrate;
