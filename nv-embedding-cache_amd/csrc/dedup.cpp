@@ -57,10 +57,10 @@ DedupBufs carve(void* ws, int64_t n) {
 
 }  // namespace
 
-// Scratch of the hash dedup-then-gather: table keys, owners, slot per key.
+// Scratch of the hash dedup-then-gather: table keys, owner per slot, slot per key.
 size_t hash_gather_bytes(int64_t n) {
   const size_t slots = hash_dedup_slots(n);
-  return pad(8 * slots) + pad(4 * slots) + pad(4 * (size_t)n) + pad(8 * (size_t)n) + 256;
+  return pad(8 * slots) + pad(4 * slots) + pad(4 * (size_t)n);
 }
 
 // Batches up to this size take the hash path (slot numbers fit 32 bits).
@@ -146,12 +146,8 @@ void dedup_gather_run(int key_bytes, int64_t n, const void* keys, const uint8_t*
     uint32_t* owner = reinterpret_cast<uint32_t*>(p);
     p += pad(4 * slots);
     uint32_t* slot_of = reinterpret_cast<uint32_t*>(p);
-    p += pad(4 * (size_t)n);
-    uint64_t* owners = reinterpret_cast<uint64_t*>(p);
-    p += pad(8 * (size_t)n);
-    uint32_t* count = reinterpret_cast<uint32_t*>(p);
     NVE_HIP(launch_hash_dedup_gather(keys, key_bytes, n, table, num_rows, row_bytes, out, out_stride, tab,
-                                     owner, slot_of, owners, count, s));
+                                     owner, slot_of, s));
     return;
   }
   DedupBufs b = carve(ws, n);

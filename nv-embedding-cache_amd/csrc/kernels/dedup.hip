@@ -10,12 +10,12 @@
 // stable inverse map and exclusive offsets.
 //
 // dedup-then-gather needs no order, so it dedups by hashing instead of
-// sorting (four launches instead of eleven): every distinct key of a
+// sorting (three launches instead of eleven): every distinct key of a
 // workgroup claims a slot of an open-addressed table (linear probing, at most
-// half full) with one compare-and-swap, the winner becoming the key's owner;
-// the owners copy their row from the table (each distinct row read once),
-// then every other position copies its owner's output row (UnpackDedup,
-// cuda_utils.cuh:24-79).
+// half full) with one compare-and-swap, the winner becoming the key's owner
+// and its workgroup copying the key's table row to the owner's output row at
+// once (each distinct row read once); then every other position copies its
+// owner's output row (UnpackDedup, cuda_utils.cuh:24-79).
 #include "device_common.cuh"
 #include "dedup_launch.hpp"
 #include "position_grad.cuh"
@@ -279,12 +279,11 @@ constexpr KT empty_slot() {
   return (KT)~(KT)0;
 }
 
-// the table's keys to empty, and the owner count to 0
+// the table's keys to empty
 template <typename KT>
-__global__ __launch_bounds__(256) void hash_clear_kernel(KT* tab, int64_t slots, uint32_t* count) {
+__global__ __launch_bounds__(256) void hash_clear_kernel(KT* tab, int64_t slots) {
   constexpr int64_t per = 16 / sizeof(KT);  // slots per 16-byte store
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i == 0) *count = 0;
   if ((i + 1) * per <= slots) {
     u32x4 e{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
     reinterpret_cast<u32x4*>(tab)[i] = e;
@@ -324,121 +323,154 @@ __device__ __forceinline__ uint32_t claim(KT* tab, KT k, int bits, bool* won) {
   }
 }
 
-constexpr int kInsertThreads = 1024;  // one key per thread
-constexpr int kLocalBits = 11;        // 2048 LDS slots per workgroup, at most half full
-
-// An owner's entry of the compact list: with 32-bit keys the key and the
-// position packed (so the copy needs no further load), else the position.
-template <typename KT>
-__device__ __forceinline__ uint64_t owner_entry(KT k, uint32_t pos) {
-  return sizeof(KT) == 4 ? ((uint64_t)k << 32) | pos : (uint64_t)pos;
-}
-
-// Each workgroup first dedups its 1024 keys in an LDS table, so a key claims
-// its global slot once per workgroup rather than once per occurrence:
-// thousands of device-scope compare-and-swaps on one hot key's slot would
-// serialize at the memory side.  The global winner of a slot owns the key:
-// it records itself in owner[slot] and in the compact owner list (one
-// atomic add per workgroup for the list's positions; per-workgroup segments
-// of the list, which need none, made the owners' copy slower: 12.1 -> 17.4 us
-// on 262,144 Zipf keys).
-template <typename KT>
-__global__ __launch_bounds__(kInsertThreads) void hash_insert_kernel(const void* keys, int key_bytes,
-                                                                     int64_t n, uint64_t num_rows, KT* tab,
-                                                                     uint32_t* owner, int bits,
-                                                                     uint32_t* slot_of, uint64_t* owners,
-                                                                     uint32_t* count) {
-  __shared__ KT lkey[1 << kLocalBits];
-  __shared__ uint32_t lslot[1 << kLocalBits];  // global slot of the local entry
-  __shared__ uint32_t wave_owners[kInsertThreads / 64];
-  __shared__ uint32_t list_base;
-  const int tid = threadIdx.x;
-  for (int j = tid; j < (1 << kLocalBits); j += kInsertThreads) lkey[j] = empty_slot<KT>();
-  __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * kInsertThreads + tid;
-  bool in = false;
-  KT k = 0;
-  if (i < n) {
-    const uint64_t k64 = (uint64_t)load_key(keys, key_bytes, i);
-    in = k64 < num_rows;  // keys outside the table get no slot and no output row
-    k = (KT)k64;
-  }
-  uint32_t ls = 0;
-  bool local_first = false;
-  if (in) ls = claim<KT>(lkey, k, kLocalBits, &local_first);
-  __syncthreads();
-  bool global_owner = false;
-  if (local_first) {
-    const uint32_t gs = claim<KT>(tab, k, bits, &global_owner);
-    lslot[ls] = gs;
-    if (global_owner) owner[gs] = (uint32_t)i;
-  }
-  // compact owner list: ranks inside the wave, wave totals, one atomic per workgroup
-  const uint64_t ballot = __ballot(global_owner);
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const uint32_t below = (uint32_t)__popcll(ballot & (lane == 0 ? 0ull : (~0ull >> (64 - lane))));
-  if (lane == 0) wave_owners[wave] = (uint32_t)__popcll(ballot);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t total = 0;
-    for (int w = 0; w < kInsertThreads / 64; ++w) {
-      const uint32_t c = wave_owners[w];
-      wave_owners[w] = total;
-      total += c;
-    }
-    list_base = total ? atomicAdd(count, total) : 0u;
-  }
-  __syncthreads();
-  if (global_owner) owners[list_base + wave_owners[wave] + below] = owner_entry<KT>(k, (uint32_t)i);
-  if (i < n) slot_of[i] = in ? lslot[ls] : kNoSlot;
-}
-
-// PASS 0: the owners (owners[0 .. *count)) copy their key's table row to
-// their output row; PASS 1: every other position copies its owner's output
-// row.  A wave resolves T positions (one per lane), then groups of G lanes
-// move one row each, U rows in flight, VB bytes per lane and load.
-struct HashCopy {
+struct HashClaim {
   const void* keys;
   int key_bytes;
   int64_t n;
+  uint64_t num_rows;
+  void* tab;
+  int bits;
+  uint32_t* owner;    // owner[slot]: position that owns the slot's key
+  uint32_t* slot_of;  // slot_of[i]: slot of position i's key (kNoSlot: out of range)
   const uint8_t* table;
+  uint64_t row_bytes;
+  uint8_t* out;
+  int64_t out_stride;
+  int g_shift;  // 2^g_shift lanes move one row
+  int passes;   // row pieces of 2^g_shift * VB bytes
+};
+
+constexpr int kClaimThreads = 1024;  // one key per thread
+constexpr int kLocalBits = 11;       // 2048 LDS slots per workgroup, at most half full
+
+// The claims and the owners' copies in one launch.  Each workgroup first
+// dedups its 1024 keys in an LDS table, so a key claims its global slot once
+// per workgroup rather than once per occurrence (device-scope
+// compare-and-swaps on one hot key's slot serialize at the memory side).  The
+// global winner of a slot owns the key: it records itself in owner[slot], and
+// its workgroup then copies the key's table row to the owner's output row --
+// each distinct row is read once.  Rows move as in the plain gather:
+// 2^g_shift lanes per row, U rows in flight per lane group, every load of a
+// round issued before any store.  Measured on 262,144 Zipf(1.05) keys, this
+// launch and the repeats' take 39 us where separate claim, owner-list and
+// owner-copy launches took 48; chunks of 512 or 2048 keys per workgroup were
+// slower (41 and 42 us), and so was reading a slot before its
+// compare-and-swap (43 us: the workgroups reach the hot keys' slots together).
+template <typename KT, int VB, int U>
+__global__ __launch_bounds__(kClaimThreads) void hash_claim_copy_kernel(HashClaim a) {
+  __shared__ KT lkey[1 << kLocalBits];
+  __shared__ uint32_t lslot[1 << kLocalBits];  // global slot of the local entry
+  __shared__ uint64_t win_row[kClaimThreads];  // the workgroup's wins: table row
+  __shared__ uint32_t win_pos[kClaimThreads];  // ... and output row
+  __shared__ uint32_t wave_wins[kClaimThreads / 64];
+  __shared__ uint32_t num_wins;
+  const int tid = threadIdx.x;
+  for (int j = tid; j < (1 << kLocalBits); j += kClaimThreads) lkey[j] = empty_slot<KT>();
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kClaimThreads + tid;
+  bool in = false;
+  KT k = 0;
+  if (i < a.n) {
+    const uint64_t k64 = (uint64_t)load_key(a.keys, a.key_bytes, i);
+    in = k64 < a.num_rows;  // keys outside the table get no slot and no output row
+    k = (KT)k64;
+  }
+  uint32_t ls = 0;
+  bool first = false;
+  if (in) ls = claim<KT>(lkey, k, kLocalBits, &first);
+  __syncthreads();
+  bool won = false;
+  if (first) {
+    const uint32_t gs = claim<KT>(static_cast<KT*>(a.tab), k, a.bits, &won);
+    lslot[ls] = gs;
+    if (won) a.owner[gs] = (uint32_t)i;
+  }
+  // the wins listed in LDS: ranks inside the wave, then wave offsets
+  const uint64_t ballot = __ballot(won);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t below = (uint32_t)__popcll(ballot & (lane == 0 ? 0ull : (~0ull >> (64 - lane))));
+  if (lane == 0) wave_wins[wave] = (uint32_t)__popcll(ballot);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t total = 0;
+    for (int w = 0; w < kClaimThreads / 64; ++w) {
+      const uint32_t c = wave_wins[w];
+      wave_wins[w] = total;
+      total += c;
+    }
+    num_wins = total;
+  }
+  __syncthreads();
+  if (won) {
+    const uint32_t q = wave_wins[wave] + below;
+    win_row[q] = (uint64_t)k;
+    win_pos[q] = (uint32_t)i;
+  }
+  if (i < a.n) a.slot_of[i] = in ? lslot[ls] : kNoSlot;
+  __syncthreads();
+  const int nw = (int)num_wins;
+  const int G = 1 << a.g_shift;
+  const int gl = lane & (G - 1);
+  const int grp = lane >> a.g_shift;
+  const int groups = 64 >> a.g_shift;
+  const int step = (kClaimThreads / 64) * groups * U;  // wins per round of the workgroup
+  const uint64_t zero_row = (uint64_t)g_zero_row;
+  for (int p = 0; p < a.passes; ++p) {
+    const int64_t off = ((int64_t)p * G + gl) * VB;
+    const bool in_row = off < (int64_t)a.row_bytes;
+    for (int q0 = wave * groups * U; q0 < nw; q0 += step) {
+      uint64_t src[U];
+      uint32_t dst[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = q0 + u * groups + grp;
+        const bool real = q < nw && in_row;
+        src[u] = real ? (uint64_t)a.table + win_row[q] * a.row_bytes + off : zero_row + (off & kZeroRowMask);
+        dst[u] = real ? win_pos[q] : kNoSlot;
+      }
+      Vec<VB> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = load_vec<VB>(src[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (dst[u] == kNoSlot) continue;
+        store_vec<VB, false>(a.out + (int64_t)dst[u] * a.out_stride + off, v[u]);
+      }
+    }
+  }
+}
+
+// Every position that does not own its key copies its owner's output row
+// (written by the claims' launch).  A wave resolves T positions (one per
+// lane), then groups of G lanes move one row each, U rows in flight, VB
+// bytes per lane and load.
+struct HashRepeat {
+  int64_t n;
   uint64_t row_bytes;
   const uint32_t* slot_of;
   const uint32_t* owner;
-  const uint64_t* owners;
-  const uint32_t* count;
   uint8_t* out;
   int64_t out_stride;
 };
 
-template <int VB, int U, int PASS, bool PACKED>
-__global__ __launch_bounds__(256) void hash_copy_kernel(HashCopy a, int g_shift, int t_shift,
-                                                        int passes) {
+template <int VB, int U>
+__global__ __launch_bounds__(256) void hash_repeat_kernel(HashRepeat a, int g_shift, int t_shift, int passes) {
   const int T = 1 << t_shift;
   const int lane = threadIdx.x & 63;
   const int64_t tile = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t base = tile << t_shift;
-  const int64_t limit = PASS == 0 ? (int64_t)*a.count : a.n;
-  if (base >= limit) return;  // whole wave past the end
+  if (base >= a.n) return;  // whole wave past the end
   const int64_t j = base + lane;
-  uint64_t src = 0;   // row to copy from, 0: nothing to do for this lane's position
-  uint32_t dst = 0;   // output row
-  if (lane < T && j < limit) {
-    if (PASS == 0) {
-      const uint64_t e = a.owners[j];
-      dst = (uint32_t)e;
-      const uint64_t key = PACKED ? e >> 32 : (uint64_t)load_key(a.keys, a.key_bytes, dst);
-      src = (uint64_t)a.table + key * a.row_bytes;
-    } else {
-      dst = (uint32_t)j;
-      const uint32_t sl = a.slot_of[j];
-      if (sl != kNoSlot) {
-        const uint32_t own = a.owner[sl];
-        if (own != (uint32_t)j) src = (uint64_t)a.out + (uint64_t)own * (uint64_t)a.out_stride;
-      }
+  uint64_t src = 0;  // row to copy from, 0: nothing to do for this lane's position
+  if (lane < T && j < a.n) {
+    const uint32_t sl = a.slot_of[j];
+    if (sl != kNoSlot) {
+      const uint32_t own = a.owner[sl];
+      if (own != (uint32_t)j) src = (uint64_t)a.out + (uint64_t)own * (uint64_t)a.out_stride;
     }
   }
+  const uint32_t dst = (uint32_t)j;
   const int G = 1 << g_shift;
   const int gl = lane & (G - 1);
   const int grp = lane >> g_shift;
@@ -484,26 +516,12 @@ size_t hash_dedup_key_bytes(int64_t num_rows) { return (uint64_t)num_rows <= 0xf
 
 hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, const uint8_t* table,
                                     int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride,
-                                    void* tab, uint32_t* owner, uint32_t* slot_of, uint64_t* owners,
-                                    uint32_t* count, hipStream_t stream) {
+                                    void* tab, uint32_t* owner, uint32_t* slot_of, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const int64_t slots = (int64_t)hash_dedup_slots(n);
   int bits = 0;
   while ((1ll << bits) < slots) ++bits;
   const bool k32 = hash_dedup_key_bytes(num_rows) == 4;
-  if (k32) {
-    hipLaunchKernelGGL(hash_clear_kernel<uint32_t>, dim3((slots / 4 + 255) / 256), dim3(256), 0, stream,
-                       static_cast<uint32_t*>(tab), slots, count);
-    hipLaunchKernelGGL(hash_insert_kernel<uint32_t>, dim3((n + kInsertThreads - 1) / kInsertThreads),
-                       dim3(kInsertThreads), 0, stream, keys, key_bytes, n, (uint64_t)num_rows,
-                       static_cast<uint32_t*>(tab), owner, bits, slot_of, owners, count);
-  } else {
-    hipLaunchKernelGGL(hash_clear_kernel<uint64_t>, dim3((slots / 2 + 255) / 256), dim3(256), 0, stream,
-                       static_cast<uint64_t*>(tab), slots, count);
-    hipLaunchKernelGGL(hash_insert_kernel<uint64_t>, dim3((n + kInsertThreads - 1) / kInsertThreads),
-                       dim3(kInsertThreads), 0, stream, keys, key_bytes, n, (uint64_t)num_rows,
-                       static_cast<uint64_t*>(tab), owner, bits, slot_of, owners, count);
-  }
   // widest vector every row, output row and base is aligned to
   int vb = 16;
   while (vb > 1 && (row_bytes % vb || out_stride % vb || (uintptr_t)table % vb || (uintptr_t)out % vb))
@@ -521,18 +539,25 @@ hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, 
   const int64_t waves = (n + tkeys - 1) / tkeys;
   const int64_t grid = (waves * 64 + 255) / 256;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  HashCopy c{keys, key_bytes, n, table, (uint64_t)row_bytes, slot_of, owner, owners, count,
-             static_cast<uint8_t*>(out), out_stride};
-#define HC(V)                                                                                          \
-  do {                                                                                                 \
-    if (k32)                                                                                           \
-      hipLaunchKernelGGL((hash_copy_kernel<V, U, 0, true>), dim3(grid), dim3(256), 0, stream, c, gs,   \
-                         ts, passes);                                                                  \
-    else                                                                                               \
-      hipLaunchKernelGGL((hash_copy_kernel<V, U, 0, false>), dim3(grid), dim3(256), 0, stream, c, gs,  \
-                         ts, passes);                                                                  \
-    hipLaunchKernelGGL((hash_copy_kernel<V, U, 1, false>), dim3(grid), dim3(256), 0, stream, c, gs,    \
-                       ts, passes);                                                                    \
+  const dim3 claim_grid((unsigned)((n + kClaimThreads - 1) / kClaimThreads));
+  HashClaim c{keys, key_bytes, n, (uint64_t)num_rows, tab, bits, owner, slot_of, table, (uint64_t)row_bytes,
+              static_cast<uint8_t*>(out), out_stride, gs, passes};
+  HashRepeat r{n, (uint64_t)row_bytes, slot_of, owner, static_cast<uint8_t*>(out), out_stride};
+  if (k32)
+    hipLaunchKernelGGL(hash_clear_kernel<uint32_t>, dim3((slots / 4 + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(tab), slots);
+  else
+    hipLaunchKernelGGL(hash_clear_kernel<uint64_t>, dim3((slots / 2 + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint64_t*>(tab), slots);
+#define HC(V)                                                                                           \
+  do {                                                                                                  \
+    if (k32)                                                                                            \
+      hipLaunchKernelGGL((hash_claim_copy_kernel<uint32_t, V, U>), claim_grid, dim3(kClaimThreads), 0,  \
+                         stream, c);                                                                    \
+    else                                                                                                \
+      hipLaunchKernelGGL((hash_claim_copy_kernel<uint64_t, V, U>), claim_grid, dim3(kClaimThreads), 0,  \
+                         stream, c);                                                                    \
+    hipLaunchKernelGGL((hash_repeat_kernel<V, U>), dim3(grid), dim3(256), 0, stream, r, gs, ts, passes); \
   } while (0)
   switch (vb) {
     case 16: HC(16); break;

@@ -44,12 +44,10 @@ size_t hash_dedup_slots(int64_t n);
 size_t hash_dedup_key_bytes(int64_t num_rows);
 // out row i = table row keys[i] for keys in [0, num_rows) (others untouched),
 // deduplicated by hashing.  Scratch: tab (hash_dedup_slots(n) keys of
-// hash_dedup_key_bytes(num_rows) bytes), owner (one word per slot), slot_of
-// (n words), owners (n 8-byte entries), count (one word).  Four launches,
-// asynchronous.
+// hash_dedup_key_bytes(num_rows) bytes), owner (one word per slot) and
+// slot_of (n words).  Three launches, asynchronous.
 hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, const uint8_t* table,
                                     int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride,
-                                    void* tab, uint32_t* owner, uint32_t* slot_of, uint64_t* owners,
-                                    uint32_t* count, hipStream_t stream);
+                                    void* tab, uint32_t* owner, uint32_t* slot_of, hipStream_t stream);
 
 }  // namespace nve_amd

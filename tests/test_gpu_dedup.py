@@ -205,3 +205,28 @@ def test_dedup_gather_reuses_a_workspace_across_batches():
                   dim * 4, vp(ws), wb, stream_ptr())
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), np.ascontiguousarray(tb).reshape(rows, -1).view(np.uint8)[keys])
+
+
+@pytest.mark.parametrize("case", ["wide_rows", "wide_keys"])
+def test_dedup_gather_wide_rows_and_64_bit_table_keys(case):
+    """Rows wider than one lane group's 1 KiB (each row copied in several
+    pieces, by the owners and by the repeats), and a table that declares
+    more than 2^32 rows, whose hash slots hold 64-bit keys (every key of the
+    batch indexes the table's first rows, which are the ones allocated)."""
+    rng = np.random.default_rng(31)
+    n = 9000
+    if case == "wide_rows":
+        rows, width, declared = 700, 2064, 700  # 129 16-byte pieces: 3 pieces per lane group
+    else:
+        rows, width, declared = 3000, 64, 2**33 + 5
+    tb = rng.integers(0, 256, size=(rows, width), dtype=np.uint8)
+    keys = (O.power_law(rng.random(n), 1, rows, 1.05) % rows).astype(np.int64)
+    keys[::97] = rng.integers(0, rows, size=keys[::97].size)
+    d_tab, d_keys = to_dev(tb.reshape(-1)), to_dev(keys)
+    out = torch.full((n, width), 0x3C, dtype=torch.uint8, device="cuda")
+    ws, wb = workspace(n)
+    ws.fill_(0x11)
+    _lib.call("nve_amd_dedup_gather", _lib.KEY_INT64, n, vp(d_keys), vp(d_tab), declared, width, vp(out),
+              width, vp(ws), wb, stream_ptr())
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), tb[keys])
