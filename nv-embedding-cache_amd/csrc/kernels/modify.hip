@@ -40,8 +40,21 @@ __global__ __launch_bounds__(256) void hist_prep_kernel(const void* keys, int ke
 }
 
 // heads[i] = 1 where a run of equal sorted keys starts
+// span_part (optional, nparts words): workgroup 0 also ORs the sort's span
+// parts into *span_out.
 __global__ __launch_bounds__(256) void run_heads_kernel(const uint64_t* ks, int64_t n,
-                                                        uint32_t* heads) {
+                                                        uint32_t* heads, const uint64_t* span_part,
+                                                        int64_t nparts, unsigned long long* span_out) {
+  if (span_part != nullptr && blockIdx.x == 0) {  // uniform over the workgroup
+    uint64_t x = 0;
+    for (int64_t j = threadIdx.x; j < nparts; j += blockDim.x) x |= span_part[j];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x |= __shfl_xor(x, o);
+    __shared__ uint64_t red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) *span_out = red[0] | red[1] | red[2] | red[3];
+  }
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) heads[i] = (i == 0 || ks[i] != ks[i - 1]) ? 1u : 0u;
 }
@@ -292,9 +305,11 @@ hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t
   return hipGetLastError();
 }
 
-hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream) {
+hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream,
+                            const uint64_t* span_part, int64_t nparts, unsigned long long* span_out) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(run_heads_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, n, heads);
+  hipLaunchKernelGGL(run_heads_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, ks, n, heads,
+                     span_part, nparts, span_out);
   return hipGetLastError();
 }
 

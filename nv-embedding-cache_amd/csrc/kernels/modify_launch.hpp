@@ -33,7 +33,11 @@ struct ReplaceLaunch {
 
 hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t* k64, uint32_t* v,
                             hipStream_t stream);
-hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream);
+// heads[i] = 1 where a run of equal sorted keys starts; with span_part
+// (nparts words, e.g. a raw sort pass's tile spans) also *span_out = their OR.
+hipError_t launch_run_heads(const uint64_t* ks, int64_t n, uint32_t* heads, hipStream_t stream,
+                            const uint64_t* span_part = nullptr, int64_t nparts = 0,
+                            unsigned long long* span_out = nullptr);
 hipError_t launch_run_gather(const uint64_t* ks, const uint32_t* vs, const uint32_t* scan, int64_t n,
                              uint32_t* start, uint64_t* ukey, uint32_t* first, hipStream_t stream);
 hipError_t launch_count_key(const uint32_t* start, uint32_t u_n, uint64_t* k2, uint32_t* v2,

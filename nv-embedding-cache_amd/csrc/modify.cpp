@@ -12,9 +12,14 @@
 //                queued on the table's registered lookup streams, copy the
 //                rows, commit the tags (ec_set_associative_device_modify.cuh:
 //                225-288, :428-451)
-// The host reads three counts back (unique keys, represented sets, records),
-// where the reference also synchronizes (gather_keys_data_ptrs.cuh:168,
-// ec_set_associative_modify.cuh:489, ec_set_associative_device_modify.cuh:443).
+// The host reads two counts back (unique keys, represented sets) and waits
+// once for the invalidation, where the reference also synchronizes
+// (gather_keys_data_ptrs.cuh:168, ec_set_associative_modify.cuh:489,
+// ec_set_associative_device_modify.cuh:443).  The key sort first assumes that
+// the keys differ only below bit kInsertSpecBits (rows of tables up to 2^32:
+// four 8-bit passes, as many as 25 to 32 exact bits take) and learns whether
+// they did with the unique count; a batch whose keys differ higher up is
+// sorted again on its exact bits.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -27,6 +32,16 @@
 namespace nve_amd {
 
 namespace {
+
+constexpr int kInsertSpecBits = 32;
+
+// Read back after the histogram's first sort: unique keys, and the OR over
+// the keys of key ^ key[0] (the bits where they differ).
+struct InsertHead {
+  uint32_t uniq;
+  uint32_t pad;
+  unsigned long long span;
+};
 
 int bits_for(uint64_t max_value) {
   int b = 0;
@@ -104,10 +119,12 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
 
   // ---- scratch (grow-only, per context) ----
   const size_t un = (size_t)n;
-  const size_t bytes = 16 * 256 + un * (8 * 2 + 4 * 2) * 3 + un * (4 * 4 + 8 * 4) +
-                       radix_sort_temp_bytes(n) + 64 * 256;
+  const size_t bytes = 18 * 256 + un * (8 * 2 + 4 * 2) * 3 + un * (4 * 4 + 8 * 4) +
+                       (size_t)radix_tiles(n) * 8 + radix_sort_temp_bytes(n) + 64 * 256;
   uint8_t* p = static_cast<uint8_t*>(ctx.buffer("insert_scratch", bytes));
   unsigned long long* d_span = carve<unsigned long long>(p, 1);
+  InsertHead* head = carve<InsertHead>(p, 1);
+  uint64_t* span_part = carve<uint64_t>(p, (size_t)radix_tiles(n));
   uint32_t* d_count = carve<uint32_t>(p, 4);
   uint64_t* ka = carve<uint64_t>(p, un);
   uint32_t* va = carve<uint32_t>(p, un);
@@ -128,17 +145,31 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   void* sort_tmp = carve<uint8_t>(p, radix_sort_temp_bytes(n));
 
   // ---- (1) histogram ----
-  NVE_HIP(launch_hist_prep(d_keys, key_bytes_, n, ka, va, s));
-  NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(d_span), 1, 0, s));
-  NVE_HIP(key_span(ka, n, d_span, s));
-  const unsigned long long span = read_back(d_span, s);
   int alt = 0;
-  NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, bits_for(span), sort_tmp, &alt, s));
+  uint32_t uniq = 0;
+  bool exact = n < 2;  // one key: nothing to sort, the exact path sorts nothing
+  if (!exact) {
+    // the first pass reads the caller's keys and writes each tile's span part
+    const RadixSource src{d_keys, key_bytes_, 1, span_part};
+    NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, kInsertSpecBits, sort_tmp, &alt, s, &src));
+    NVE_HIP(launch_run_heads(alt ? kb : ka, n, heads, s, span_part, radix_tiles(n), &head->span));
+    NVE_HIP(exclusive_scan_u32(heads, n, &head->uniq, sort_tmp, s));
+    const InsertHead h = read_back(head, s);
+    exact = (h.span >> kInsertSpecBits) != 0;
+    uniq = h.uniq;
+  }
+  if (exact) {
+    NVE_HIP(launch_hist_prep(d_keys, key_bytes_, n, ka, va, s));
+    NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(d_span), 1, 0, s));
+    NVE_HIP(key_span(ka, n, d_span, s));
+    const unsigned long long span = read_back(d_span, s);
+    NVE_HIP(radix_sort_pairs(ka, va, kb, vb, n, 0, bits_for(span), sort_tmp, &alt, s));
+    NVE_HIP(launch_run_heads(alt ? kb : ka, n, heads, s));
+    NVE_HIP(exclusive_scan_u32(heads, n, d_count, sort_tmp, s));
+    uniq = read_u32(d_count, s);
+  }
   uint64_t* ks = alt ? kb : ka;
   uint32_t* vs = alt ? vb : va;
-  NVE_HIP(launch_run_heads(ks, n, heads, s));
-  NVE_HIP(exclusive_scan_u32(heads, n, d_count, sort_tmp, s));
-  const uint32_t uniq = read_u32(d_count, s);
   NVE_HIP(launch_run_gather(ks, vs, heads, n, start, ukey, first, s));
   // sort the runs by count descending (stable: ties keep ascending key order)
   uint64_t* k2 = alt ? ka : kb;  // the buffers not holding ks / vs

@@ -87,6 +87,39 @@ def test_insert_all_ties_and_duplicates():
     ct.close()
 
 
+@pytest.mark.parametrize("case", ["below_bit_32", "bit_32_once", "wide_int64", "negative_int32", "single_key"])
+def test_insert_key_sort_bits_first_assumed_then_checked(case):
+    """The histogram's key sort first assumes that the keys differ only below
+    bit 32 (four 8-bit passes, no host round trip before them) and checks that
+    with the unique count; keys that differ higher up are sorted again on
+    their exact bits.  Cache keys are any integers, not only row indices."""
+    rng = np.random.default_rng(["below_bit_32", "bit_32_once", "wide_int64", "negative_int32",
+                                 "single_key"].index(case) + 40)
+    rows, dim = 4000, 8
+    uvm = float_table(rng, rows, dim, O.F32)
+    kb = 4 if case == "negative_int32" else 8
+    ct = CachedTable(uvm, 64 * 1024, kb)
+    n = 3000
+    base = rng.zipf(1.2, size=n) % 700
+    if case == "below_bit_32":
+        keys = (base * 6_000_011 % (2**32)).astype(np.int64)
+        keys[:2] = [0, 2**32 - 1]
+    elif case == "bit_32_once":
+        keys = (base * 6_000_011 % (2**32)).astype(np.int64)
+        keys[n // 2] = 2**32
+    elif case == "wide_int64":
+        keys = (base.astype(np.int64) * 0x1E3779B97F4A7C15 % (2**62)).astype(np.int64) - 2**61
+    elif case == "negative_int32":
+        keys = (base - 350).astype(np.int32) * 3_000_017
+    else:
+        keys = np.array([2**40 + 3], np.int64)
+    vals = rng.integers(0, 256, size=(keys.size, ct.width), dtype=np.uint8)
+    table_insert(ct, keys, vals, ct.width)
+    ct.model.insert_keys(keys, values=vals.reshape(-1), value_stride=ct.width)
+    assert_same_state(ct)
+    ct.close()
+
+
 def test_insert_values_use_first_occurrence_and_padded_stride():
     rng = np.random.default_rng(9)
     rows, dim = 2000, 12
