@@ -241,15 +241,22 @@ __global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
   const float rc = g8f(cv, 7 - x);
   const uint32_t num_repl = cnt < 8 ? cnt : 8;
   const bool write = ((uint32_t)x < num_repl) && (best > rc);
-  if (write) {
-    const uint32_t slot = atomicAdd(a.num_records, 1u);
-    if (slot < a.max_records) {
+  // records at the set's own positions of the order: lane x's at base + x
+  // (x < num_repl <= cnt), every other position of the set marked empty (a
+  // counter of records bumped by each replacing wave serialized thousands of
+  // same-address atomics at the memory side: 70 us per 262,144-key insert)
+  if ((uint32_t)x < cnt) {
+    const uint32_t pos = base + x;
+    if (write) {
       const int64_t key = a.hkeys[best_pos];
-      a.rec_slot[slot] = (uint64_t)set * 8 + rd;
-      a.rec_tag[slot] = (int64_t)(K)((UK)(K)key / ns);  // embed_cache_construct_tag
-      a.rec_src[slot] = a.hsrc[best_pos];
+      a.rec_slot[pos] = (uint64_t)set * 8 + rd;
+      a.rec_tag[pos] = (int64_t)(K)((UK)(K)key / ns);  // embed_cache_construct_tag
+      a.rec_src[pos] = a.hsrc[best_pos];
+    } else {
+      a.rec_slot[pos] = kNoRecord;
     }
   }
+  for (uint32_t j = 8 + x; j < cnt; j += 8) a.rec_slot[base + j] = kNoRecord;
   // the replaced way's counter becomes the winner's priority
   for (int sl = 0; sl < 8; ++sl) {
     const int wr = __shfl((int)write, sl, 8);
@@ -268,8 +275,8 @@ template <typename K>
 __global__ __launch_bounds__(256) void invalidate_kernel(const uint32_t* num, uint32_t max_records,
                                                          const uint64_t* slot, K* tags, K sentinel) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t n = *num < max_records ? *num : max_records;
-  if (i < n) tags[slot[i]] = sentinel;
+  const uint32_t n = num != nullptr && *num < max_records ? *num : max_records;
+  if (i < n && slot[i] != kNoRecord) tags[slot[i]] = sentinel;
 }
 
 template <typename K>
@@ -277,8 +284,8 @@ __global__ __launch_bounds__(256) void commit_kernel(const uint32_t* num, uint32
                                                      const uint64_t* slot, const int64_t* tag,
                                                      K* tags) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t n = *num < max_records ? *num : max_records;
-  if (i < n) tags[slot[i]] = (K)tag[i];
+  const uint32_t n = num != nullptr && *num < max_records ? *num : max_records;
+  if (i < n && slot[i] != kNoRecord) tags[slot[i]] = (K)tag[i];
 }
 
 // one wave per record: 16-byte (or 4 / 1 byte) chunks of the row
@@ -288,8 +295,8 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* num, uin
                                                         uint8_t* data, uint64_t row_bytes) {
   const int64_t rec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
-  const uint32_t n = *num < max_records ? *num : max_records;
-  if (rec >= n) return;
+  const uint32_t n = num != nullptr && *num < max_records ? *num : max_records;
+  if (rec >= n || slot[rec] == kNoRecord) return;
   const uint8_t* s = reinterpret_cast<const uint8_t*>(src[rec]);
   uint8_t* d = data + slot[rec] * row_bytes;
   for (uint64_t o = (uint64_t)lane * VB; o < row_bytes; o += 64 * VB)

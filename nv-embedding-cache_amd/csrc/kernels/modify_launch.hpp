@@ -24,12 +24,18 @@ struct ReplaceLaunch {
   int64_t decay_len;
   uint64_t num_sets;
   int64_t sentinel;
-  uint32_t* num_records;     // atomic record counter (zeroed by the caller)
-  uint32_t max_records;
-  uint64_t* rec_slot;        // set*8 + way
+  // Records, one per position of the candidate order: position roff[r] + x
+  // holds set r's x-th replacement, and every position without one holds
+  // kNoRecord as its slot (a set replaces at most min(its candidates, 8) ways,
+  // so its records fit its own range of the order).
+  uint32_t max_records;      // positions (the length of order)
+  uint64_t* rec_slot;        // set*8 + way, or kNoRecord
   int64_t* rec_tag;          // new tag
   uint64_t* rec_src;         // source row address
 };
+
+// rec_slot of a record position that holds no record
+constexpr uint64_t kNoRecord = ~0ull;
 
 hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t* k64, uint32_t* v,
                             hipStream_t stream);
@@ -50,6 +56,8 @@ hipError_t launch_hist_gather(const uint32_t* order, const uint32_t* start, cons
 hipError_t launch_set_gather(const uint64_t* ks, const uint32_t* scan, int64_t m, uint32_t* rset,
                              uint32_t* roff, hipStream_t stream);
 hipError_t launch_set_replace(const ReplaceLaunch& a, int key_bytes, hipStream_t stream);
+// The record kernels take records [0, min(*num, max_records)), or with num
+// null [0, max_records); records whose slot is kNoRecord are skipped.
 hipError_t launch_invalidate(const uint32_t* num, uint32_t max_records, const uint64_t* slot,
                              void* tags, int key_bytes, int64_t sentinel, hipStream_t stream);
 hipError_t launch_commit(const uint32_t* num, uint32_t max_records, const uint64_t* slot,

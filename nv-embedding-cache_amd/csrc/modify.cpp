@@ -201,7 +201,6 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
 
   // ---- (3) replacement ----
   ++global_ts_;  // once per insert (ec_set_associative_device_modify.cuh:262)
-  NVE_HIP(launch_fill_u32(d_count + 1, 1, 0, s));
   ReplaceLaunch r{};
   r.rset = rset;
   r.roff = roff;
@@ -219,7 +218,6 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   r.decay_len = decay_len_;
   r.num_sets = num_sets_;
   r.sentinel = cfg_.invalid_key;
-  r.num_records = d_count + 1;
   r.max_records = m;
   r.rec_slot = rec_slot;
   r.rec_tag = rec_tag;
@@ -227,7 +225,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   NVE_HIP(launch_set_replace(r, key_bytes_, s));
 
   // ---- (4) invalidate -> drain -> copy -> commit ----
-  NVE_HIP(launch_invalidate(d_count + 1, m, rec_slot, tags_, key_bytes_, cfg_.invalid_key, s));
+  NVE_HIP(launch_invalidate(nullptr, m, rec_slot, tags_, key_bytes_, cfg_.invalid_key, s));
   // Lookups queued from here on see the invalidated tags (the invalidation is
   // complete before the host goes on); lookups queued earlier may still read
   // the old rows of those ways, so the copy waits for them
@@ -235,9 +233,9 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   lookups_->order_before(s);
   uintptr_t align = (uintptr_t)rows | (uintptr_t)row_stride;
   const int src_align = (align % 16 == 0) ? 16 : (align % 4 == 0) ? 4 : 1;
-  NVE_HIP(launch_copy_rows(d_count + 1, m, rec_slot, rec_src, src_align, data_,
+  NVE_HIP(launch_copy_rows(nullptr, m, rec_slot, rec_src, src_align, data_,
                            (uint64_t)cfg_.row_size_in_bytes, s));
-  NVE_HIP(launch_commit(d_count + 1, m, rec_slot, rec_tag, tags_, key_bytes_, s));
+  NVE_HIP(launch_commit(nullptr, m, rec_slot, rec_tag, tags_, key_bytes_, s));
   NVE_HIP(hipStreamSynchronize(s));
 }
 
