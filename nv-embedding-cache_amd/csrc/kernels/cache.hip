@@ -65,12 +65,14 @@ hipError_t launch_fill_u64(uint64_t* p, int64_t count, uint64_t v, hipStream_t s
 // become 0 for the next count.
 __global__ __launch_bounds__(64) void counter_total_kernel(unsigned long long* words, int n,
                                                            unsigned long long* total, int reset) {
-  if (threadIdx.x != 0) return;
   unsigned long long t = 0;
-  for (int i = 0; i < n; ++i) t += words[i];
-  if (reset)
-    for (int i = 0; i < n; ++i) words[i] = 0;
-  *total = t;
+  for (int i = (int)threadIdx.x; i < n; i += 64) {
+    t += words[i];
+    if (reset) words[i] = 0;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+  if (threadIdx.x == 0) *total = t;
 }
 
 hipError_t launch_counter_total(unsigned long long* words, int n, unsigned long long* host_total, int reset,

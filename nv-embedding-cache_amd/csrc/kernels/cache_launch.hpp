@@ -11,7 +11,7 @@ hipError_t launch_fill_tags(void* tags, int64_t count, int key_bytes, int64_t se
 hipError_t launch_fill_u32(uint32_t* p, int64_t count, uint32_t v, hipStream_t stream);
 hipError_t launch_fill_u64(uint64_t* p, int64_t count, uint64_t v, hipStream_t stream);
 // *host_total = sum of words[0..n) (host_total: pinned host memory, written by
-// the kernel); reset != 0 also zeroes the words.  One thread.
+// the kernel); reset != 0 also zeroes the words.  One wave.
 hipError_t launch_counter_total(unsigned long long* words, int n, unsigned long long* host_total, int reset,
                                 hipStream_t stream);
 hipError_t launch_cache_erase(void* tags, const void* keys, int64_t n, int key_bytes,

@@ -375,10 +375,13 @@ constexpr int kZeroRowBytes = 4096;
 constexpr int64_t kZeroRowMask = kZeroRowBytes - 1;
 static __device__ __align__(16) uint8_t g_zero_row[kZeroRowBytes + 64] = {};
 
-// Miss counters are kMissStripes words; a workgroup adds to word
-// blockIdx.x % kMissStripes and readers add the words up: thousands of
-// atomics on one address serialize in one memory channel.
+// Miss counters are kMissStripes words, each at the start of its own 128-byte
+// line (kMissStripeWords apart); a workgroup adds to stripe
+// blockIdx.x % kMissStripes and readers add the words up: same-address (and
+// same-line) atomics serialize at the memory side, thousands of them per
+// launch when every wave adds its misses.
 constexpr int kMissStripes = 8;
+constexpr int kMissStripeWords = 16;
 
 // Adds the wave's per-lane miss counts to the workgroup's counter word (every
 // lane active).
@@ -386,7 +389,7 @@ __device__ __forceinline__ void add_misses(unsigned long long* counter, uint32_t
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
   if (__lane_id() == 0 && n)
-    atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)n);
+    atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)) * kMissStripeWords, (unsigned long long)n);
 }
 
 // ---------------------------------------------------------------------------

@@ -132,7 +132,7 @@ struct SplitCacheArgs : SplitArgs {
   const uint8_t* cache_data;
   const void* cache_tags;
   uint64_t num_sets;
-  unsigned long long* miss_counter;  // optional, kMissStripes words
+  unsigned long long* miss_counter;  // optional, kMissStripes * kMissStripeWords words
 };
 
 constexpr uint32_t kBackingRow = 0x80000000u;  // code bit: a backing-table row, not a cache slot
@@ -187,7 +187,7 @@ __device__ __forceinline__ void add_group_misses(unsigned long long* counter, ui
   if (threadIdx.x == 0) {
     uint32_t m = 0;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m += wave_misses[w];
-    if (m) atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)), (unsigned long long)m);
+    if (m) atomicAdd(counter + (blockIdx.x & (kMissStripes - 1)) * kMissStripeWords, (unsigned long long)m);
   }
 }
 

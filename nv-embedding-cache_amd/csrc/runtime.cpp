@@ -287,11 +287,12 @@ int64_t ExecutionContext::take_misses() {
 }
 
 int64_t read_miss_words(const unsigned long long* counter, hipStream_t stream) {
-  unsigned long long w[kMissCounterWords];
-  read_small(w, counter, sizeof(w), stream);
-  unsigned long long t = 0;
-  for (int i = 0; i < kMissCounterWords; ++i) t += w[i];
-  return (int64_t)t;
+  // the sum is written by a kernel into a pinned per-thread word
+  thread_local unsigned long long* slot = nullptr;
+  if (slot == nullptr) NVE_HIP(hipHostMalloc((void**)&slot, 64, hipHostMallocDefault));
+  NVE_HIP(launch_counter_total(const_cast<unsigned long long*>(counter), kMissCounterWords, slot, 0, stream));
+  NVE_HIP(hipStreamSynchronize(stream));
+  return (int64_t)*static_cast<volatile unsigned long long*>(slot);
 }
 
 void ExecutionContext::add_pending(std::future<void> f) {

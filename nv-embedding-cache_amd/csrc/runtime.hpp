@@ -225,9 +225,10 @@ const void* host_input(ExecutionContext& ctx, const char* name, const void* p, s
 // `stream`.  The copy lands in a pinned per-thread slot first: a pageable
 // destination costs a staged copy, tens of microseconds for a few bytes.
 void read_small(void* host, const void* dev, size_t bytes, hipStream_t stream);
-// Words of a device miss counter (the kernels stripe their atomics over them;
-// kMissStripes in the kernels) and their sum, read like read_small.
-constexpr int kMissCounterWords = 8;
+// Words of a device miss counter: the kernels stripe their atomics over 8
+// words 16 apart, one per 128-byte line (kMissStripes, kMissStripeWords in
+// the kernels); readers add up every word, the others staying 0.
+constexpr int kMissCounterWords = 8 * 16;
 int64_t read_miss_words(const unsigned long long* counter, hipStream_t stream);
 
 template <typename T>
