@@ -510,7 +510,7 @@ def run_workload(args, torch, _lib):
         _lib.call("nve_context_wait", ctx)
         _lib.call("nve_context_destroy", ctx)
         _lib.call("nve_layer_destroy", layer)
-        kernel = ("hash dedup + gather: hash_clear, hash_insert, hash_copy (owners), hash_copy (repeats)"
+        kernel = ("hash dedup + gather: hash_clear, hash_claim_copy (claims + owners' rows), hash_repeat"
                   if w == "c2" else "gather_realign_kernel (dequant)")
     elif w == "c3":
         # LinearUVM: pinned host table + 32 GiB 8-way HBM cache, warmed by 10
