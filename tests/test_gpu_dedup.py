@@ -230,3 +230,43 @@ def test_dedup_gather_wide_rows_and_64_bit_table_keys(case):
               width, vp(ws), wb, stream_ptr())
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), tb[keys])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_dedup_gather_random_shapes(seed):
+    """Seeded random batches: sizes across workgroup edges, row widths from 2
+    bytes to several pieces per lane group, padded output strides, uniform /
+    Zipf / out-of-range / single-key batches, int32 and int64 keys, and a
+    workspace holding arbitrary bytes; every output row must be the table's
+    row of its key, and rows of keys outside the table untouched."""
+    rng = np.random.default_rng(500 + seed)
+    for _ in range(6):
+        n = int(rng.choice([1, 2, 1023, 1025, 4097])) if rng.random() < 0.3 else int(rng.integers(1, 120_000))
+        rows = int(rng.integers(1, 100_000))
+        width = int(rng.choice([2, 6, 16, 64, 256, 260, 1040, 2064]))
+        stride = width + int(rng.choice([0, 0, 16, 2]))
+        kind = int(rng.integers(0, 4))
+        if kind == 0:
+            keys = rng.integers(0, rows, size=n)
+        elif kind == 1:
+            keys = (rng.zipf(1.05 + rng.random(), size=n) - 1) % rows
+        elif kind == 2:
+            keys = rng.integers(-5, rows + 5, size=n)
+        else:
+            keys = np.full(n, rng.integers(0, rows))
+        kdt = np.int32 if rng.random() < 0.3 else np.int64
+        keys = keys.astype(kdt)
+        tb = rng.integers(0, 256, size=(rows, width), dtype=np.uint8)
+        d_tab, d_keys = to_dev(tb.reshape(-1)), to_dev(keys)
+        out = torch.full((n, stride), 0x5A, dtype=torch.uint8, device="cuda")
+        ws, wb = workspace(n)
+        ws.fill_(int(rng.integers(0, 256)))
+        kt = _lib.KEY_INT32 if kdt == np.int32 else _lib.KEY_INT64
+        _lib.call("nve_amd_dedup_gather", kt, n, vp(d_keys), vp(d_tab), rows, width, vp(out), stride, vp(ws), wb,
+                  stream_ptr())
+        torch.cuda.synchronize()
+        k64 = keys.astype(np.int64)
+        ok = (k64 >= 0) & (k64 < rows)
+        exp = np.full((n, stride), 0x5A, np.uint8)
+        exp[ok, :width] = tb[k64[ok]]
+        assert np.array_equal(out.cpu().numpy(), exp), (n, rows, width, stride, kind, kdt)
