@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
         const K tw = tags[w];
         if ((K)((UK)tw * ns + (UK)set) == key) hit_ways |= 1u << w;
       }
-      if (hit_ways == 0) {
+      if (hit_ways == 0 && (a.src_rows == 0 || (uint64_t)(int64_t)key < a.src_rows)) {
         hpos = loc;
         hp = prio;
       }

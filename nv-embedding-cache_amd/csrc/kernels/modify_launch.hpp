@@ -24,6 +24,10 @@ struct ReplaceLaunch {
   int64_t decay_len;
   uint64_t num_sets;
   int64_t sentinel;
+  // insert_from_uvm: rows of the backing table; a key outside [0, src_rows)
+  // has no source row and is no candidate (a resident one still gains its
+  // priority).  0: every key is a candidate (rows come with the keys).
+  uint64_t src_rows;
   // Records, one per position of the candidate order: position roff[r] + x
   // holds set r's x-th replacement, and every position without one holds
   // kNoRecord as its slot (a set replaces at most min(its candidates, 8) ways,

@@ -218,6 +218,7 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   r.decay_len = decay_len_;
   r.num_sets = num_sets_;
   r.sentinel = cfg_.invalid_key;
+  r.src_rows = from_uvm ? (uint64_t)cfg_.uvm_num_rows : 0;  // keys past the backing table: no candidates
   r.max_records = m;
   r.rec_slot = rec_slot;
   r.rec_tag = rec_tag;

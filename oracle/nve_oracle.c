@@ -853,7 +853,9 @@ static int64_t replace_one_set(orc_cache* c, uint32_t set, const int64_t* cand, 
             hit = 1;
           }
         }
-        if (!hit) {
+        /* a candidate without a source row (a key outside the backing table
+         * of insert_from_uvm) is not inserted; a resident one still gains */
+        if (!hit && (src_rows == NULL || src_rows[loc] != NULL)) {
           pos2[x] = (uint32_t)loc;
           hp2[x] = priority[loc];
         }
@@ -944,7 +946,7 @@ int64_t orc_cache_insert_hist(orc_cache* c, const int64_t* ukeys, const float* p
 }
 
 int64_t orc_cache_insert_keys(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
-                              const uint8_t* values, int64_t value_stride,
+                              uint64_t uvm_rows, const uint8_t* values, int64_t value_stride,
                               int64_t max_modify_size) {
   if (n <= 0) return 0;
   int64_t* uk = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
@@ -954,7 +956,10 @@ int64_t orc_cache_insert_keys(orc_cache* c, const void* keys, int64_t n, const u
   const int64_t m = (u < max_modify_size) ? u : max_modify_size;
   const uint8_t** rows = (const uint8_t**)malloc(sizeof(uint8_t*) * (size_t)(m > 0 ? m : 1));
   for (int64_t i = 0; i < m; i++) {
-    rows[i] = uvm ? uvm + (uint64_t)uk[i] * (uint64_t)c->row_bytes : values + fi[i] * value_stride;
+    if (uvm)
+      rows[i] = (uint64_t)uk[i] < uvm_rows ? uvm + (uint64_t)uk[i] * (uint64_t)c->row_bytes : NULL;
+    else
+      rows[i] = values + fi[i] * value_stride;
   }
   const int64_t r = orc_cache_insert_hist(c, uk, pr, rows, m, NULL, NULL);
   free(rows);
@@ -1080,6 +1085,9 @@ int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* p
       }
     }
     if (hit) continue;
+    /* a key outside the backing table of insert_from_uvm has no source row:
+     * it is not a candidate */
+    if (src_rows != NULL && src_rows[i] == NULL) continue;
     int wmin = 0; /* std::min_element: the first smallest counter */
     for (int w = 1; w < ORC_WAYS; w++)
       if (sc[w] < sc[wmin]) wmin = w;
@@ -1106,7 +1114,7 @@ int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* p
 }
 
 int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
-                                   const uint8_t* values, int64_t value_stride,
+                                   uint64_t uvm_rows, const uint8_t* values, int64_t value_stride,
                                    int64_t max_modify_size) {
   if (n <= 0) return 0;
   int64_t* uk = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
@@ -1114,8 +1122,12 @@ int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, co
   int64_t* fi = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
   const int64_t u = orc_histogram_host(keys, c->key_bytes, n, uk, pr, fi);
   const uint8_t** rows = (const uint8_t**)malloc(sizeof(uint8_t*) * (size_t)u);
-  for (int64_t i = 0; i < u; i++)
-    rows[i] = uvm ? uvm + (uint64_t)uk[i] * (uint64_t)c->row_bytes : values + fi[i] * value_stride;
+  for (int64_t i = 0; i < u; i++) {
+    if (uvm)
+      rows[i] = (uint64_t)uk[i] < uvm_rows ? uvm + (uint64_t)uk[i] * (uint64_t)c->row_bytes : NULL;
+    else
+      rows[i] = values + fi[i] * value_stride;
+  }
   const int64_t r = orc_cache_insert_host(c, uk, pr, rows, u, max_modify_size, NULL, NULL);
   free(rows);
   free(fi);

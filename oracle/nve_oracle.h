@@ -178,10 +178,14 @@ int64_t orc_cache_insert_hist(orc_cache* c, const int64_t* ukeys, const float* p
                               const uint8_t* const* src_rows, int64_t m, int64_t* out_set,
                               int64_t* out_way);
 
-/* Convenience: histogram + insert, rows from a dense table (insert_from_uvm) when
- * uvm != NULL, else from values + first_idx*stride (GpuTable::insert). */
+/* Convenience: histogram + insert, rows from a dense table of uvm_rows rows
+ * (insert_from_uvm) when uvm != NULL, else from values + first_idx*stride
+ * (GpuTable::insert).  A key outside [0, uvm_rows) has no source row and is not
+ * a candidate (resident, it still gains its priority); the reference would
+ * read past the table.  In orc_cache_insert_hist and orc_cache_insert_host,
+ * likewise, a NULL entry of a non-NULL src_rows is no candidate. */
 int64_t orc_cache_insert_keys(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
-                              const uint8_t* values, int64_t value_stride,
+                              uint64_t uvm_rows, const uint8_t* values, int64_t value_stride,
                               int64_t max_modify_size);
 
 /* Invalidate (erase) keys: every way whose key matches gets the sentinel tag. */
@@ -214,9 +218,10 @@ int64_t orc_cache_insert_host(orc_cache* c, const int64_t* ukeys, const float* p
                               int64_t* out_set, int64_t* out_way);
 
 /* Convenience for the host-metadata cache: orc_histogram_host + insert, rows
- * from a dense table when uvm != NULL, else values + first_idx*stride. */
+ * from a dense table of uvm_rows rows when uvm != NULL (keys outside it are no
+ * candidates), else values + first_idx*stride. */
 int64_t orc_cache_insert_keys_host(orc_cache* c, const void* keys, int64_t n, const uint8_t* uvm,
-                                   const uint8_t* values, int64_t value_stride,
+                                   uint64_t uvm_rows, const uint8_t* values, int64_t value_stride,
                                    int64_t max_modify_size);
 
 /* ---- training backprop (GradientCalculator::compute_gradients,

@@ -92,7 +92,7 @@ def _declare(L):
     L.orc_pooling_backprop.restype = I64
     L.orc_pooling_backprop.argtypes = [P, I32, I64, I32, I32, P, I64, I64, P, I32, P, I32, I64, I64, P, P]
     L.orc_cache_insert_keys_host.restype = I64
-    L.orc_cache_insert_keys_host.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, P, I64, I64]
+    L.orc_cache_insert_keys_host.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, U64, P, I64, I64]
     L.orc_cache_set.restype = ctypes.c_uint32
     L.orc_cache_set.argtypes = [ctypes.POINTER(OrcCache), I64]
     L.orc_cache_tag.restype = I64
@@ -108,7 +108,7 @@ def _declare(L):
     L.orc_cache_insert_hist.restype = I64
     L.orc_cache_insert_hist.argtypes = [ctypes.POINTER(OrcCache), P, P, P, I64, P, P]
     L.orc_cache_insert_keys.restype = I64
-    L.orc_cache_insert_keys.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, P, I64, I64]
+    L.orc_cache_insert_keys.argtypes = [ctypes.POINTER(OrcCache), P, I64, P, U64, P, I64, I64]
     L.orc_cache_erase.restype = I64
     L.orc_cache_erase.argtypes = [ctypes.POINTER(OrcCache), P, I64]
     L.orc_dedup.restype = I64
@@ -309,10 +309,12 @@ class Cache:
         return rows, hits, misses
 
     def insert_keys(self, keys, uvm=None, values=None, value_stride=0, max_modify_size=1 << 20):
-        """GpuTable::insert / insert_from_uvm with this cache's policy."""
+        """GpuTable::insert / insert_from_uvm with this cache's policy; uvm is
+        the backing table's bytes (its row count = uvm.size / row_bytes)."""
         keys = np.ascontiguousarray(keys, self.kdt)
+        uvm_rows = 0 if uvm is None else np.asarray(uvm).nbytes // self.row_bytes
         fn = lib().orc_cache_insert_keys_host if self.host_modify else lib().orc_cache_insert_keys
-        return fn(ctypes.byref(self.c), _p(keys), keys.size, _p(uvm), _p(values), value_stride,
+        return fn(ctypes.byref(self.c), _p(keys), keys.size, _p(uvm), uvm_rows, _p(values), value_stride,
                   max_modify_size)
 
     def insert_hist_host(self, ukeys, priority, src_ptrs=None, max_update=1 << 20):

@@ -201,3 +201,36 @@ def test_uvm_layer_auto_insert_raises_hit_rate_and_keeps_results():
     _lib.call("nve_context_destroy", lctx)
     _lib.call("nve_layer_destroy", layer)
     ct.close()
+
+
+@pytest.mark.parametrize("modify_on_gpu", [True, False])
+@pytest.mark.parametrize("key_bytes", [8, 4])
+def test_insert_from_uvm_keys_outside_the_backing_table(modify_on_gpu, key_bytes):
+    """insert_from_uvm with keys below 0 or past the backing table: they have
+    no source row and are never inserted (the reference would read past the
+    table), while a resident one of them (put there by an insert with values)
+    still gains its priority, under both policies."""
+    rng = np.random.default_rng(61 + key_bytes + (0 if modify_on_gpu else 7))
+    rows, dim = 3000, 16
+    uvm = float_table(rng, rows, dim, O.F32, dyadic_values=False)
+    ct = CachedTable(uvm, 48 * 1024, key_bytes, modify_on_gpu=modify_on_gpu)
+    kdt = np.int64 if key_bytes == 8 else np.int32
+    outside = np.array([rows + 5, -3], kdt)
+    vals = rng.integers(0, 256, size=(outside.size, ct.width), dtype=np.uint8)
+    table_insert(ct, outside[:1], vals[:1], ct.width)  # rows + 5 resident with its own values
+    ct.model.insert_keys(outside[:1], values=vals[:1].reshape(-1), value_stride=ct.width)
+    assert_same_state(ct)
+    for step in range(3):
+        keys = (rng.zipf(1.2, size=2500) % (rows + 400) - 100).astype(kdt)  # about 17 % outside
+        keys[::50] = outside[step % 2]
+        d_keys = to_dev(keys)
+        _lib.call("nve_amd_table_insert_from_uvm", ct.table, ct.ctx, keys.size, vp(d_keys))
+        ct.model.insert_keys(keys, uvm=ct.uvm_np.reshape(-1))
+        assert_same_state(ct)
+        tags = ct.model.tags()
+        ways = np.nonzero(tags != -1)[0]
+        resident = tags[ways] * ct.num_sets + ways // 8  # key = tag * num_sets + set
+        assert np.all(((resident >= 0) & (resident < rows)) | (resident == rows + 5))
+    assert ct.model.find_way(rows + 5) >= 0
+    assert ct.model.find_way(-3) < 0
+    ct.close()

@@ -232,3 +232,22 @@ def test_power_law_range_and_skew():
     c = np.bincount(y, minlength=1000)
     # Zipf-like: frequency decreases with the index, index 1 is the mode
     assert c[1] == c.max() and c[1] > 5 * c[100]
+
+
+@pytest.mark.parametrize("host_modify", [False, True])
+def test_insert_from_uvm_skips_keys_without_a_source_row(host_modify):
+    """Closed form on an empty cache with room for every key: insert_from_uvm
+    makes exactly the distinct keys inside the backing table resident, with
+    their rows; keys below 0 or past the table never become resident."""
+    rows, width = 500, 16
+    uvm = np.arange(rows * width, dtype=np.uint32).astype(np.uint8).reshape(rows, width)
+    c = O.Cache(2_000_000, width, 8, host_modify=host_modify)
+    keys = np.array([3, 3, 499, 500, 501, -1, -7, 42, 10_000, 42], np.int64)
+    c.insert_keys(keys, uvm=uvm.reshape(-1))
+    tags = c.tags()
+    ways = np.nonzero(tags != -1)[0]
+    resident = set((tags[ways] * c.num_sets + ways // 8).tolist())
+    assert resident == {3, 42, 499}
+    for k in (3, 42, 499):
+        slot = c.set_of(k) * 8 + c.find_way(k)
+        assert np.array_equal(c.data().reshape(-1, width)[slot], uvm[k])
