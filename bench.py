@@ -660,6 +660,48 @@ def run_workload(args, torch, _lib):
             cfg_out["insert_us"] = {"median": round(ins[len(ins) // 2], 1), "min": round(ins[0], 1),
                                     "max": round(ins[-1], 1), "calls": len(ins), "keys_per_call": nkeys}
             log(f"c3: insert of a {nkeys}-key batch: median {ins[len(ins) // 2]:.1f} us over {len(ins)} calls")
+        if args.c3_update_steps > 0:
+            # the cache's update and update_accumulate of a whole batch (every key
+            # resident) on a cache-only table of the same rows (4 GiB, no backing
+            # table to write through to): records of the ways, invalidate, order
+            # after the lookups, copy or add the rows, commit
+            ucfg = _lib.load().nve_gpu_table_config_default()
+            ucfg.cache_size = 4 << 30
+            ucfg.row_size_in_bytes = width
+            ucfg.value_dtype = _lib.DT_F16
+            utab = ctypes.c_void_p()
+            _lib.call("nve_gpu_table_create", ctypes.byref(utab), _lib.KEY_INT64, ctypes.byref(ucfg), None)
+            uctx = ctypes.c_void_p()
+            _lib.call("nve_table_create_execution_context", utab, ctypes.byref(uctx), sp, sp, None, None)
+            ukeys = torch.randperm(rows, device="cuda")[:nkeys].to(torch.int64)
+            uvals = torch.empty((nkeys, dim), dtype=torch.float16, device="cuda").normal_(0.0, 0.02)
+            kp, vp_ = ctypes.c_void_p(ukeys.data_ptr()), ctypes.c_void_p(uvals.data_ptr())
+            _lib.call("nve_table_insert", utab, uctx, nkeys, kp, width, width, vp_)
+            _lib.call("nve_context_wait", uctx)
+            upd = {}
+            for name in ("update", "update_accumulate"):
+                ts = []
+                for i in range(args.c3_update_steps + 1):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    if name == "update":
+                        _lib.call("nve_table_update", utab, uctx, nkeys, kp, width, width, vp_)
+                    else:
+                        _lib.call("nve_table_update_accumulate", utab, uctx, nkeys, kp, width, width, vp_,
+                                  _lib.DT_F16)
+                    _lib.call("nve_context_wait", uctx)
+                    torch.cuda.synchronize()
+                    if i:  # the first call sizes its scratch
+                        ts.append((time.perf_counter() - t0) * 1e6)
+                ts.sort()
+                upd[name] = {"median": round(ts[len(ts) // 2], 1), "min": round(ts[0], 1), "calls": len(ts)}
+                log(f"c3: cache {name} of a {nkeys}-key batch: median {ts[len(ts) // 2]:.1f} us over {len(ts)} calls")
+            upd["table"] = "cache-only GpuTable, 4 GiB, fp16 x 128, every key resident"
+            upd["keys_per_call"] = nkeys
+            cfg_out["cache_update_us"] = upd
+            _lib.call("nve_context_destroy", uctx)
+            _lib.call("nve_table_destroy", utab)
+            del ukeys, uvals
         # HBM: keys + 8 tags (64 B) per key + cached rows; host link: missed rows
         alg = (nkeys * (8 + 64) + int(nkeys * hit) * width + int(nkeys * (1 - hit)) * width
                + (nkeys if concat else bags) * width)
@@ -825,6 +867,8 @@ def main():
     ap.add_argument("--c3-concat", action="store_true", help="c3: one row per key instead of pooled bags")
     ap.add_argument("--c3-hotness", type=int, default=1024, choices=[16, 32, 64, 128, 256, 512, 1024],
                     help="c3: keys per pooled bag (262,144 keys per batch in 262,144 / hotness bags)")
+    ap.add_argument("--c3-update-steps", type=int, default=5,
+                    help="c3: timed update / update_accumulate calls of a whole batch on a cache-only table")
     ap.add_argument("--c3-keys", type=int, default=262144,
                     help="c3: keys per batch (a multiple of --c3-hotness)")
     ap.add_argument("--c3-no-touch", action="store_true",

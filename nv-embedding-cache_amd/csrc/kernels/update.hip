@@ -17,32 +17,41 @@
 // once: two fp16 values add exactly in fp32 unless their exponents differ by
 // more than 13, and then the smaller is below a quarter ulp of the larger).
 #include "device_common.cuh"
+#include "modify_launch.hpp"
 #include "update_launch.hpp"
 
 namespace nve_amd {
 
+// Record i belongs to key i: the way holding it (a key holds at most one way:
+// the insert policies never place a resident key again), or kNoRecord.  A
+// counter of records bumped by every wave serialized the waves' atomics at
+// the memory side.
 template <typename K, typename UK>
 __global__ __launch_bounds__(256) void update_records_kernel(
     const K* keys, int64_t n, const K* tags, UK num_sets, const uint8_t* values,
-    int64_t value_stride, uint32_t* num_records, uint32_t max_records, uint64_t* rec_slot,
-    int64_t* rec_tag, uint64_t* rec_src) {
+    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const K key = keys[i];
   const UK set = (UK)key % num_sets;
   const K* t = tags + (uint64_t)set * 8;
+  int way = -1;
+  K tag = 0;
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
+  for (int w = 7; w >= 0; --w) {
     const K tw = t[w];
     if ((K)((UK)tw * num_sets + set) == key) {
-      const uint32_t r = atomicAdd(num_records, 1u);
-      if (r < max_records) {
-        rec_slot[r] = (uint64_t)set * 8 + w;
-        rec_tag[r] = (int64_t)tw;
-        rec_src[r] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
-      }
+      way = w;
+      tag = tw;
     }
   }
+  if (way < 0) {
+    rec_slot[i] = kNoRecord;
+    return;
+  }
+  rec_slot[i] = (uint64_t)set * 8 + (uint64_t)way;
+  rec_tag[i] = (int64_t)tag;
+  rec_src[i] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
 }
 
 // *p (a 32-bit word holding fp16 element `half` at bits 16*half) += v.
@@ -59,11 +68,39 @@ __device__ __forceinline__ void atomic_add_f16(uint32_t* word, int half, uint16_
   }
 }
 
+// The 32-bit word at *word += the two fp16 elements of v (low half to low
+// half), each sum computed in fp32 and rounded to nearest even once.
+__device__ __forceinline__ void atomic_add_f16x2(uint32_t* word, uint32_t v) {
+  uint32_t old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (true) {
+    const uint16_t lo = f2h(h2f((uint16_t)old) + h2f((uint16_t)v));
+    const uint16_t hi = f2h(h2f((uint16_t)(old >> 16)) + h2f((uint16_t)(v >> 16)));
+    const uint32_t nw = ((uint32_t)hi << 16) | lo;
+    const uint32_t seen = atomicCAS(word, old, nw);
+    if (seen == old) return;
+    old = seen;
+  }
+}
+
 // dst[0..elems) += src[0..elems) in the float type T (fp32 or fp16 bits).
+// fp16 rows whose destination and length are 4-byte aligned are added a word
+// (two elements) per lane: lanes updating the two halves of one word would
+// otherwise retry each other's compare-and-swaps.
 template <bool F16>
 __device__ __forceinline__ void add_row(uint8_t* dst, const uint8_t* src, uint64_t row_bytes,
                                         int lane, int lanes) {
   if constexpr (F16) {
+    if ((((uint64_t)dst | row_bytes) & 3u) == 0) {
+      const uint64_t words = row_bytes / 4;
+      for (uint64_t e = lane; e < words; e += lanes) {
+        const uint64_t sa = (uint64_t)src + 4 * e;
+        const uint32_t v = (sa & 3u) == 0 ? gload<uint32_t>(sa)
+                                          : (uint32_t)gload<uint16_t>(sa) |
+                                                ((uint32_t)gload<uint16_t>(sa + 2) << 16);
+        atomic_add_f16x2(reinterpret_cast<uint32_t*>(dst) + e, v);
+      }
+      return;
+    }
     const uint64_t elems = row_bytes / 2;
     for (uint64_t e = lane; e < elems; e += lanes) {
       const uint64_t a = (uint64_t)dst + 2 * e;
@@ -87,8 +124,8 @@ __global__ __launch_bounds__(256) void accumulate_rows_kernel(const uint32_t* nu
                                                               const uint64_t* src, uint8_t* data,
                                                               uint64_t row_bytes) {
   const int64_t rec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const uint32_t n = *num < max_records ? *num : max_records;
-  if (rec >= n) return;
+  const uint32_t n = num != nullptr && *num < max_records ? *num : max_records;
+  if (rec >= n || slot[rec] == kNoRecord) return;
   add_row<F16>(data + slot[rec] * row_bytes, reinterpret_cast<const uint8_t*>(src[rec]), row_bytes,
                threadIdx.x & 63, 64);
 }
@@ -134,18 +171,18 @@ int copy_vb(const void* a, const void* b, int64_t stride, uint64_t row_bytes) {
 
 hipError_t launch_update_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                  uint64_t num_sets, const uint8_t* values, int64_t value_stride,
-                                 uint32_t* num_records, uint32_t max_records, uint64_t* rec_slot,
-                                 int64_t* rec_tag, uint64_t* rec_src, hipStream_t stream) {
+                                 uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
+                                 hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (key_bytes == 4)
     hipLaunchKernelGGL((update_records_kernel<int32_t, uint32_t>), grid, dim3(256), 0, stream,
                        (const int32_t*)keys, n, (const int32_t*)tags, (uint32_t)num_sets, values,
-                       value_stride, num_records, max_records, rec_slot, rec_tag, rec_src);
+                       value_stride, rec_slot, rec_tag, rec_src);
   else
     hipLaunchKernelGGL((update_records_kernel<int64_t, uint64_t>), grid, dim3(256), 0, stream,
                        (const int64_t*)keys, n, (const int64_t*)tags, (uint64_t)num_sets, values,
-                       value_stride, num_records, max_records, rec_slot, rec_tag, rec_src);
+                       value_stride, rec_slot, rec_tag, rec_src);
   return hipGetLastError();
 }
 

@@ -8,16 +8,16 @@
 
 namespace nve_amd {
 
-// One record per way holding a key of keys[0..n): slot set*8+way, the way's
-// current tag, and the address of the key's update row (values + i*stride).
-// *num_records (zeroed by the caller) counts every match; records past
-// max_records are dropped.
+// Record i for key i of keys[0..n): the slot set*8+way of the way holding
+// it, the way's current tag and the address of the key's update row
+// (values + i*stride); kNoRecord as the slot when the key is not resident.
 hipError_t launch_update_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                  uint64_t num_sets, const uint8_t* values, int64_t value_stride,
-                                 uint32_t* num_records, uint32_t max_records, uint64_t* rec_slot,
-                                 int64_t* rec_tag, uint64_t* rec_src, hipStream_t stream);
+                                 uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
+                                 hipStream_t stream);
 
-// Adds the update row of each record to its cache slot, element by element in
+// Adds the update row of each record (as launch_copy_rows takes them) to its
+// cache slot, element by element in
 // the table's float type (kF32 or kF16; f16 sums rounded to nearest even once
 // per addition), atomically so that repeated keys all land.
 hipError_t launch_accumulate_rows(const uint32_t* num, uint32_t max_records, const uint64_t* slot,

@@ -62,8 +62,7 @@ void GpuTable::modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, cons
                            const uint8_t* d_vals, int64_t value_stride, bool accumulate,
                            int dtype) {
   const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, cfg_.max_modify_size));
-  uint8_t* p = static_cast<uint8_t*>(ctx.buffer("update_records", 256 + (size_t)chunk * 8 * 3 + 768));
-  uint32_t* num = carve<uint32_t>(p, 1);
+  uint8_t* p = static_cast<uint8_t*>(ctx.buffer("update_records", (size_t)chunk * 8 * 3 + 768));
   uint64_t* slot = carve<uint64_t>(p, (size_t)chunk);
   int64_t* tag = carve<int64_t>(p, (size_t)chunk);
   uint64_t* src = carve<uint64_t>(p, (size_t)chunk);
@@ -73,21 +72,21 @@ void GpuTable::modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, cons
   for (int64_t k0 = 0; k0 < n; k0 += chunk) {
     const int64_t cn = std::min(chunk, n - k0);
     const uint32_t m = (uint32_t)cn;
-    NVE_HIP(launch_fill_u32(num, 1, 0, s));
+    // record i for key i (empty when the key is not resident)
     NVE_HIP(launch_update_records(static_cast<const uint8_t*>(d_keys) + k0 * key_bytes_, cn,
                                   key_bytes_, tags_, num_sets_, d_vals + k0 * value_stride,
-                                  value_stride, num, m, slot, tag, src, s));
-    NVE_HIP(launch_invalidate(num, m, slot, tags_, key_bytes_, cfg_.invalid_key, s));
+                                  value_stride, slot, tag, src, s));
+    NVE_HIP(launch_invalidate(nullptr, m, slot, tags_, key_bytes_, cfg_.invalid_key, s));
     // lookups queued before the invalidation may still read these rows
     NVE_HIP(hipStreamSynchronize(s));
     lookups_->order_before(s);
     if (accumulate)
-      NVE_HIP(launch_accumulate_rows(num, m, slot, src, data_, (uint64_t)cfg_.row_size_in_bytes,
+      NVE_HIP(launch_accumulate_rows(nullptr, m, slot, src, data_, (uint64_t)cfg_.row_size_in_bytes,
                                      dtype, s));
     else
-      NVE_HIP(launch_copy_rows(num, m, slot, src, src_align, data_,
+      NVE_HIP(launch_copy_rows(nullptr, m, slot, src, src_align, data_,
                                (uint64_t)cfg_.row_size_in_bytes, s));
-    NVE_HIP(launch_commit(num, m, slot, tag, tags_, key_bytes_, s));
+    NVE_HIP(launch_commit(nullptr, m, slot, tag, tags_, key_bytes_, s));
     NVE_HIP(hipStreamSynchronize(s));  // the records are reused by the next chunk
   }
 }

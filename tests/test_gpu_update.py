@@ -149,9 +149,12 @@ def test_table_update_accumulate(dtype):
     ct.close()
 
 
-def test_accumulate_contended_fp16_row():
-    """300 adds of 2^-9 to the same fp16 row, all at once: every add lands."""
-    rows, dim = 100, 40
+@pytest.mark.parametrize("dim", [40, 39])
+def test_accumulate_contended_fp16_row(dim):
+    """300 adds of 2^-9 to the same fp16 row, all at once: every add lands,
+    whether the row is added a 32-bit word (two elements) per lane (80-byte
+    rows) or an element per lane (78-byte rows, half of them 2-byte aligned)."""
+    rows = 100
     uvm = np.zeros((rows, dim), np.float16).view(np.uint8).reshape(rows, dim * 2)
     ct = CachedTable(uvm, 64 * 1024, 8, value_dtype=_lib.DT_F16)
     vals = np.zeros((1, dim * 2), np.uint8)
