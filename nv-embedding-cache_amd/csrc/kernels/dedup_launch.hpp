@@ -43,9 +43,11 @@ size_t hash_dedup_slots(int64_t n);
 // Bytes per hash-table key: 4 when every row index fits 32 bits, else 8.
 size_t hash_dedup_key_bytes(int64_t num_rows);
 // out row i = table row keys[i] for keys in [0, num_rows) (others untouched),
-// deduplicated by hashing.  Scratch: tab (hash_dedup_slots(n) keys of
-// hash_dedup_key_bytes(num_rows) bytes), owner (one word per slot) and
-// slot_of (n words).  Three launches, asynchronous.
+// deduplicated by hashing.  Scratch: tab (hash_dedup_slots(n) 8-byte slots:
+// key and owner position when hash_dedup_key_bytes(num_rows) is 4, else the
+// key), owner (one word per slot, 8-byte keys only) and slot_of (n words:
+// each position's owner, or with 8-byte keys its slot).  Three launches,
+// asynchronous.
 hipError_t launch_hash_dedup_gather(const void* keys, int key_bytes, int64_t n, const uint8_t* table,
                                     int64_t num_rows, int64_t row_bytes, void* out, int64_t out_stride,
                                     void* tab, uint32_t* owner, uint32_t* slot_of, hipStream_t stream);
