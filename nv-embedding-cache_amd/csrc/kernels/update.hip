@@ -22,36 +22,66 @@
 
 namespace nve_amd {
 
-// Record i belongs to key i: the way holding it (a key holds at most one way:
-// the insert policies never place a resident key again), or kNoRecord.  A
-// counter of records bumped by every wave serialized the waves' atomics at
-// the memory side.
+// The ways whose rebuilt key (tag * num_sets + set, empty ways included, as
+// the reference's SetUpdateDataKernel compares them) equals key: bit w.
+template <typename K, typename UK>
+__device__ __forceinline__ uint32_t matching_ways(const K* tags, UK num_sets, K key, UK* set_out) {
+  const UK set = (UK)key % num_sets;
+  const K* t = tags + (uint64_t)set * 8;
+  uint32_t mask = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w)
+    if ((K)((UK)t[w] * num_sets + set) == key) mask |= 1u << w;
+  *set_out = set;
+  return mask;
+}
+
+// Record i for key i: its first matching way, or kNoRecord.  A key matching
+// more than one way (only one equal to the rebuilt key of empty ways, which
+// needs num_sets to divide 2^64 or 2^32) sets *multi, a pinned host word, and
+// its further ways are recorded by update_more_records_kernel.  (A counter of
+// records bumped by every wave, as all records once took their slots,
+// serialized the waves' atomics at the memory side.)
 template <typename K, typename UK>
 __global__ __launch_bounds__(256) void update_records_kernel(
     const K* keys, int64_t n, const K* tags, UK num_sets, const uint8_t* values,
-    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src) {
+    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src, uint32_t* multi) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const K key = keys[i];
-  const UK set = (UK)key % num_sets;
-  const K* t = tags + (uint64_t)set * 8;
-  int way = -1;
-  K tag = 0;
-#pragma unroll
-  for (int w = 7; w >= 0; --w) {
-    const K tw = t[w];
-    if ((K)((UK)tw * num_sets + set) == key) {
-      way = w;
-      tag = tw;
-    }
-  }
-  if (way < 0) {
+  UK set;
+  const uint32_t mask = matching_ways<K, UK>(tags, num_sets, keys[i], &set);
+  if (mask == 0) {
     rec_slot[i] = kNoRecord;
     return;
   }
-  rec_slot[i] = (uint64_t)set * 8 + (uint64_t)way;
-  rec_tag[i] = (int64_t)tag;
+  const int w = __ffs(mask) - 1;
+  rec_slot[i] = (uint64_t)set * 8 + (uint64_t)w;
+  rec_tag[i] = (int64_t)tags[(uint64_t)set * 8 + w];
   rec_src[i] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
+  if (mask & (mask - 1)) *multi = 1u;
+}
+
+// The further matching ways of every key: records [0, *count) (count zeroed
+// by the caller), at most cap.
+template <typename K, typename UK>
+__global__ __launch_bounds__(256) void update_more_records_kernel(
+    const K* keys, int64_t n, const K* tags, UK num_sets, const uint8_t* values,
+    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src, uint32_t* count,
+    uint32_t cap) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  UK set;
+  uint32_t mask = matching_ways<K, UK>(tags, num_sets, keys[i], &set);
+  mask &= mask - 1;  // the first way has record i
+  while (mask) {
+    const int w = __ffs(mask) - 1;
+    mask &= mask - 1;
+    const uint32_t r = atomicAdd(count, 1u);
+    if (r >= cap) return;
+    rec_slot[r] = (uint64_t)set * 8 + (uint64_t)w;
+    rec_tag[r] = (int64_t)tags[(uint64_t)set * 8 + w];
+    rec_src[r] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
+  }
 }
 
 // *p (a 32-bit word holding fp16 element `half` at bits 16*half) += v.
@@ -172,17 +202,34 @@ int copy_vb(const void* a, const void* b, int64_t stride, uint64_t row_bytes) {
 hipError_t launch_update_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                  uint64_t num_sets, const uint8_t* values, int64_t value_stride,
                                  uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
-                                 hipStream_t stream) {
+                                 uint32_t* multi, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (key_bytes == 4)
     hipLaunchKernelGGL((update_records_kernel<int32_t, uint32_t>), grid, dim3(256), 0, stream,
                        (const int32_t*)keys, n, (const int32_t*)tags, (uint32_t)num_sets, values,
-                       value_stride, rec_slot, rec_tag, rec_src);
+                       value_stride, rec_slot, rec_tag, rec_src, multi);
   else
     hipLaunchKernelGGL((update_records_kernel<int64_t, uint64_t>), grid, dim3(256), 0, stream,
                        (const int64_t*)keys, n, (const int64_t*)tags, (uint64_t)num_sets, values,
-                       value_stride, rec_slot, rec_tag, rec_src);
+                       value_stride, rec_slot, rec_tag, rec_src, multi);
+  return hipGetLastError();
+}
+
+hipError_t launch_update_more_records(const void* keys, int64_t n, int key_bytes, const void* tags,
+                                      uint64_t num_sets, const uint8_t* values, int64_t value_stride,
+                                      uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
+                                      uint32_t* count, uint32_t cap, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (key_bytes == 4)
+    hipLaunchKernelGGL((update_more_records_kernel<int32_t, uint32_t>), grid, dim3(256), 0, stream,
+                       (const int32_t*)keys, n, (const int32_t*)tags, (uint32_t)num_sets, values,
+                       value_stride, rec_slot, rec_tag, rec_src, count, cap);
+  else
+    hipLaunchKernelGGL((update_more_records_kernel<int64_t, uint64_t>), grid, dim3(256), 0, stream,
+                       (const int64_t*)keys, n, (const int64_t*)tags, (uint64_t)num_sets, values,
+                       value_stride, rec_slot, rec_tag, rec_src, count, cap);
   return hipGetLastError();
 }
 

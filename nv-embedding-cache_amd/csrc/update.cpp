@@ -66,27 +66,54 @@ void GpuTable::modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, cons
   uint64_t* slot = carve<uint64_t>(p, (size_t)chunk);
   int64_t* tag = carve<int64_t>(p, (size_t)chunk);
   uint64_t* src = carve<uint64_t>(p, (size_t)chunk);
+  // set by the records kernel when a key matches more than one way
+  volatile uint32_t* multi = static_cast<volatile uint32_t*>(ctx.buffer("update_multi", 64, true));
   const int src_align = (int)(((uint64_t)d_vals | (uint64_t)value_stride) & 15u) == 0
                             ? 16
                             : ((((uint64_t)d_vals | (uint64_t)value_stride) & 3u) == 0 ? 4 : 1);
+  const uint64_t row_bytes = (uint64_t)cfg_.row_size_in_bytes;
+  auto apply = [&](const uint32_t* num, uint32_t cap, const uint64_t* sl, const uint64_t* sr) {
+    if (accumulate)
+      NVE_HIP(launch_accumulate_rows(num, cap, sl, sr, data_, row_bytes, dtype, s));
+    else
+      NVE_HIP(launch_copy_rows(num, cap, sl, sr, src_align, data_, row_bytes, s));
+  };
   for (int64_t k0 = 0; k0 < n; k0 += chunk) {
     const int64_t cn = std::min(chunk, n - k0);
     const uint32_t m = (uint32_t)cn;
-    // record i for key i (empty when the key is not resident)
-    NVE_HIP(launch_update_records(static_cast<const uint8_t*>(d_keys) + k0 * key_bytes_, cn,
-                                  key_bytes_, tags_, num_sets_, d_vals + k0 * value_stride,
-                                  value_stride, slot, tag, src, s));
+    const uint8_t* ck = static_cast<const uint8_t*>(d_keys) + k0 * key_bytes_;
+    const uint8_t* cv = d_vals + k0 * value_stride;
+    // record i for key i (empty when no way matches it)
+    *multi = 0;
+    NVE_HIP(launch_update_records(ck, cn, key_bytes_, tags_, num_sets_, cv, value_stride, slot, tag, src,
+                                  const_cast<uint32_t*>(multi), s));
     NVE_HIP(launch_invalidate(nullptr, m, slot, tags_, key_bytes_, cfg_.invalid_key, s));
     // lookups queued before the invalidation may still read these rows
     NVE_HIP(hipStreamSynchronize(s));
+    // keys matching several ways (only a key equal to the rebuilt key of the
+    // empty ways of its set): records of their further ways, invalidated too
+    uint32_t* more_num = nullptr;
+    uint64_t* more_slot = nullptr;
+    int64_t* more_tag = nullptr;
+    uint64_t* more_src = nullptr;
+    const uint32_t more_cap = (uint32_t)std::min<uint64_t>(7ull * m, 0xffffffffull);
+    if (*multi != 0) {
+      uint8_t* q = static_cast<uint8_t*>(ctx.buffer("update_more_records", 256 + (size_t)more_cap * 8 * 3 + 768));
+      more_num = carve<uint32_t>(q, 1);
+      more_slot = carve<uint64_t>(q, more_cap);
+      more_tag = carve<int64_t>(q, more_cap);
+      more_src = carve<uint64_t>(q, more_cap);
+      NVE_HIP(launch_fill_u32(more_num, 1, 0, s));
+      NVE_HIP(launch_update_more_records(ck, cn, key_bytes_, tags_, num_sets_, cv, value_stride, more_slot,
+                                         more_tag, more_src, more_num, more_cap, s));
+      NVE_HIP(launch_invalidate(more_num, more_cap, more_slot, tags_, key_bytes_, cfg_.invalid_key, s));
+      NVE_HIP(hipStreamSynchronize(s));
+    }
     lookups_->order_before(s);
-    if (accumulate)
-      NVE_HIP(launch_accumulate_rows(nullptr, m, slot, src, data_, (uint64_t)cfg_.row_size_in_bytes,
-                                     dtype, s));
-    else
-      NVE_HIP(launch_copy_rows(nullptr, m, slot, src, src_align, data_,
-                               (uint64_t)cfg_.row_size_in_bytes, s));
+    apply(nullptr, m, slot, src);
+    if (more_num != nullptr) apply(more_num, more_cap, more_slot, more_src);
     NVE_HIP(launch_commit(nullptr, m, slot, tag, tags_, key_bytes_, s));
+    if (more_num != nullptr) NVE_HIP(launch_commit(more_num, more_cap, more_slot, more_tag, tags_, key_bytes_, s));
     NVE_HIP(hipStreamSynchronize(s));  // the records are reused by the next chunk
   }
 }

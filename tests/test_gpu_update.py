@@ -278,3 +278,49 @@ def test_gpu_layer_accumulate_rejects_quantized_tables():
         _lib.call("nve_layer_accumulate", lay.layer, lay.ctx, 4, vp(keys), tb.shape[1], tb.shape[1], vp(upd),
                   _lib.DT_QI8_F32, 0)
     lay.close()
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_update_reaches_every_way_whose_rebuilt_key_matches(accumulate):
+    """An empty way's tag rebuilds to the key sentinel * num_sets + set (in
+    unsigned 64-bit arithmetic), and when num_sets divides 2^64 that key falls
+    in the same set: it then matches all eight empty ways of the set, as the
+    reference's SetUpdateDataKernel compares them, and the update writes (or
+    adds) its row into every one of them, next to an ordinary resident key."""
+    rng = np.random.default_rng(77 + int(accumulate))
+    rows, dim = 2000, 16
+    uvm = float_table(rng, rows, dim, O.F32)
+    per_set = 8 * 8 + 8 * dim * 4 + 8 * 4  # tags, rows, counters (all multiples of 16)
+    ct = CachedTable(uvm, 128 * per_set, 8)
+    assert ct.num_sets == 128
+    ct.model.insert_keys(np.array([11], np.int64), uvm=ct.uvm_np.reshape(-1))
+    ct.load_model()
+    s = 5 if ct.model.set_of(11) != 5 else 6
+    odd = s - ct.num_sets  # rebuilt key of every empty way of set s
+    # accumulate: the odd key twice (both add to every matching way); update:
+    # once (two rows copied to one way at once may interleave)
+    keys = np.array([odd, 11, odd] if accumulate else [odd, 11], np.int64)
+    upd = dyadic(rng, (keys.size, dim)).astype(np.float32)
+    tags0, _, _, rows0 = cache_state(ct)
+    d_keys, d_upd = to_dev(keys), to_dev(upd.view(np.uint8).reshape(-1))
+    if accumulate:
+        _lib.call("nve_table_update_accumulate", ct.table, ct.ctx, keys.size, vp(d_keys), dim * 4, dim * 4,
+                  vp(d_upd), _lib.DT_F32)
+    else:
+        _lib.call("nve_table_update", ct.table, ct.ctx, keys.size, vp(d_keys), dim * 4, dim * 4, vp(d_upd))
+    torch.cuda.synchronize()
+    tags1, _, _, rows1 = cache_state(ct)
+    assert np.array_equal(tags1, tags0)
+    sl11 = slot_of(tags1, ct.num_sets, 11)
+    ways = slots_of(tags1, ct.num_sets, odd)
+    assert len(ways) == 8 and sl11 not in ways
+    r11 = rows1[sl11].view(np.float32)
+    if accumulate:
+        assert np.array_equal(r11, rows0[sl11].view(np.float32) + upd[1])
+        for w in ways:  # both occurrences of the odd key add to every matching way
+            assert np.array_equal(rows1[w].view(np.float32), rows0[w].view(np.float32) + upd[0] + upd[2])
+    else:
+        assert np.array_equal(r11, upd[1])
+        for w in ways:
+            assert np.array_equal(rows1[w].view(np.float32), upd[0])
+    ct.close()
