@@ -36,6 +36,17 @@ __device__ __forceinline__ uint32_t matching_ways(const K* tags, UK num_sets, K 
   return mask;
 }
 
+// The tag a record commits: the key's own tag, key / num_sets in unsigned
+// arithmetic (the device policy, SetUpdateDataKernel
+// ec_set_associative_modify.cuh:557), or the way's current tag (the host
+// policy, ec_set_associative_host_modify.h:503-506).  The two differ only for
+// a key equal to the rebuilt key of empty ways: the device policy turns those
+// ways into ordinary tags.
+template <typename K, typename UK>
+__device__ __forceinline__ int64_t record_tag(K key, UK num_sets, K way_tag, bool own_tag) {
+  return own_tag ? (int64_t)(K)((UK)key / num_sets) : (int64_t)way_tag;
+}
+
 // Record i for key i: its first matching way, or kNoRecord.  A key matching
 // more than one way (only one equal to the rebuilt key of empty ways, which
 // needs num_sets to divide 2^64 or 2^32) sets *multi, a pinned host word, and
@@ -45,24 +56,27 @@ __device__ __forceinline__ uint32_t matching_ways(const K* tags, UK num_sets, K 
 template <typename K, typename UK>
 __global__ __launch_bounds__(256) void update_records_kernel(
     const K* keys, int64_t n, const K* tags, UK num_sets, const uint8_t* values,
-    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src, uint32_t* multi) {
+    int64_t value_stride, uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src, uint32_t* multi,
+    bool own_tag) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   UK set;
-  const uint32_t mask = matching_ways<K, UK>(tags, num_sets, keys[i], &set);
+  const K key = keys[i];
+  const uint32_t mask = matching_ways<K, UK>(tags, num_sets, key, &set);
   if (mask == 0) {
     rec_slot[i] = kNoRecord;
     return;
   }
   const int w = __ffs(mask) - 1;
   rec_slot[i] = (uint64_t)set * 8 + (uint64_t)w;
-  rec_tag[i] = (int64_t)tags[(uint64_t)set * 8 + w];
+  rec_tag[i] = record_tag<K, UK>(key, num_sets, tags[(uint64_t)set * 8 + w], own_tag);
   rec_src[i] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
   if (mask & (mask - 1)) *multi = 1u;
 }
 
 // The further matching ways of every key: records [0, *count) (count zeroed
-// by the caller), at most cap.
+// by the caller), at most cap.  Device policy only (the host policy records
+// the first matching way of a key and stops).
 template <typename K, typename UK>
 __global__ __launch_bounds__(256) void update_more_records_kernel(
     const K* keys, int64_t n, const K* tags, UK num_sets, const uint8_t* values,
@@ -71,7 +85,8 @@ __global__ __launch_bounds__(256) void update_more_records_kernel(
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   UK set;
-  uint32_t mask = matching_ways<K, UK>(tags, num_sets, keys[i], &set);
+  const K key = keys[i];
+  uint32_t mask = matching_ways<K, UK>(tags, num_sets, key, &set);
   mask &= mask - 1;  // the first way has record i
   while (mask) {
     const int w = __ffs(mask) - 1;
@@ -79,7 +94,7 @@ __global__ __launch_bounds__(256) void update_more_records_kernel(
     const uint32_t r = atomicAdd(count, 1u);
     if (r >= cap) return;
     rec_slot[r] = (uint64_t)set * 8 + (uint64_t)w;
-    rec_tag[r] = (int64_t)tags[(uint64_t)set * 8 + w];
+    rec_tag[r] = record_tag<K, UK>(key, num_sets, tags[(uint64_t)set * 8 + w], true);
     rec_src[r] = (uint64_t)values + (uint64_t)i * (uint64_t)value_stride;
   }
 }
@@ -202,17 +217,17 @@ int copy_vb(const void* a, const void* b, int64_t stride, uint64_t row_bytes) {
 hipError_t launch_update_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                  uint64_t num_sets, const uint8_t* values, int64_t value_stride,
                                  uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
-                                 uint32_t* multi, hipStream_t stream) {
+                                 uint32_t* multi, bool own_tag, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (key_bytes == 4)
     hipLaunchKernelGGL((update_records_kernel<int32_t, uint32_t>), grid, dim3(256), 0, stream,
                        (const int32_t*)keys, n, (const int32_t*)tags, (uint32_t)num_sets, values,
-                       value_stride, rec_slot, rec_tag, rec_src, multi);
+                       value_stride, rec_slot, rec_tag, rec_src, multi, own_tag);
   else
     hipLaunchKernelGGL((update_records_kernel<int64_t, uint64_t>), grid, dim3(256), 0, stream,
                        (const int64_t*)keys, n, (const int64_t*)tags, (uint64_t)num_sets, values,
-                       value_stride, rec_slot, rec_tag, rec_src, multi);
+                       value_stride, rec_slot, rec_tag, rec_src, multi, own_tag);
   return hipGetLastError();
 }
 

@@ -10,16 +10,19 @@ namespace nve_amd {
 
 // Record i for key i of keys[0..n): the slot set*8+way of its first
 // matching way (rebuilt key equal to it, empty ways included, as the
-// reference compares them), the way's current tag and the address of the
-// key's update row (values + i*stride); kNoRecord as the slot when no way
-// matches.  A key matching several ways sets *multi (a pinned host word the
-// caller zeroes): then launch_update_more_records records the further ways.
+// reference compares them), the tag to commit (own_tag: the key's own tag,
+// key / num_sets, as the device policy records it; else the way's current
+// tag, as the host policy does) and the address of the key's update row
+// (values + i*stride); kNoRecord as the slot when no way matches.  A key
+// matching several ways sets *multi (a pinned host word the caller zeroes):
+// then launch_update_more_records records the further ways.
 hipError_t launch_update_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                  uint64_t num_sets, const uint8_t* values, int64_t value_stride,
                                  uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,
-                                 uint32_t* multi, hipStream_t stream);
-// The second and later matching ways of every key of keys[0..n): records
-// [0, *count) (*count zeroed by the caller), at most cap of them.
+                                 uint32_t* multi, bool own_tag, hipStream_t stream);
+// The second and later matching ways of every key of keys[0..n) (device
+// policy: each with the key's own tag): records [0, *count) (*count zeroed
+// by the caller), at most cap of them.
 hipError_t launch_update_more_records(const void* keys, int64_t n, int key_bytes, const void* tags,
                                       uint64_t num_sets, const uint8_t* values, int64_t value_stride,
                                       uint64_t* rec_slot, int64_t* rec_tag, uint64_t* rec_src,

@@ -83,21 +83,25 @@ void GpuTable::modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, cons
     const uint32_t m = (uint32_t)cn;
     const uint8_t* ck = static_cast<const uint8_t*>(d_keys) + k0 * key_bytes_;
     const uint8_t* cv = d_vals + k0 * value_stride;
-    // record i for key i (empty when no way matches it)
+    // record i for key i (empty when no way matches it); the device policy
+    // commits the key's own tag into every matching way
+    // (ec_set_associative_modify.cuh:541-561), the host policy the first
+    // matching way's current tag (ec_set_associative_host_modify.h:489-512)
     *multi = 0;
     NVE_HIP(launch_update_records(ck, cn, key_bytes_, tags_, num_sets_, cv, value_stride, slot, tag, src,
-                                  const_cast<uint32_t*>(multi), s));
+                                  const_cast<uint32_t*>(multi), cfg_.modify_on_gpu, s));
     NVE_HIP(launch_invalidate(nullptr, m, slot, tags_, key_bytes_, cfg_.invalid_key, s));
     // lookups queued before the invalidation may still read these rows
     NVE_HIP(hipStreamSynchronize(s));
     // keys matching several ways (only a key equal to the rebuilt key of the
     // empty ways of its set): records of their further ways, invalidated too
+    // (device policy; the host policy stops at a key's first matching way)
     uint32_t* more_num = nullptr;
     uint64_t* more_slot = nullptr;
     int64_t* more_tag = nullptr;
     uint64_t* more_src = nullptr;
     const uint32_t more_cap = (uint32_t)std::min<uint64_t>(7ull * m, 0xffffffffull);
-    if (*multi != 0) {
+    if (*multi != 0 && cfg_.modify_on_gpu) {
       uint8_t* q = static_cast<uint8_t*>(ctx.buffer("update_more_records", 256 + (size_t)more_cap * 8 * 3 + 768));
       more_num = carve<uint32_t>(q, 1);
       more_slot = carve<uint64_t>(q, more_cap);

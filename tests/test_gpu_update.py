@@ -280,18 +280,25 @@ def test_gpu_layer_accumulate_rejects_quantized_tables():
     lay.close()
 
 
+@pytest.mark.parametrize("device_policy", [True, False])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_update_reaches_every_way_whose_rebuilt_key_matches(accumulate):
+def test_update_reaches_every_way_whose_rebuilt_key_matches(accumulate, device_policy):
     """An empty way's tag rebuilds to the key sentinel * num_sets + set (in
     unsigned 64-bit arithmetic), and when num_sets divides 2^64 that key falls
-    in the same set: it then matches all eight empty ways of the set, as the
-    reference's SetUpdateDataKernel compares them, and the update writes (or
-    adds) its row into every one of them, next to an ordinary resident key."""
-    rng = np.random.default_rng(77 + int(accumulate))
+    in the same set: it then matches all eight empty ways of the set.  The
+    device policy's SetUpdateDataKernel records every matching way with the
+    key's own tag, key / num_sets (ec_set_associative_modify.cuh:541-561), and
+    tag_update_kernel commits it (ec_set_associative.cuh:252-261): the eight
+    ways then hold 2^57 - 1 (128 sets), no longer the sentinel, and each gets
+    the row (or the sum).  The host policy records only the first matching way
+    and commits its current tag (ec_set_associative_host_modify.h:489-512): one
+    way gets the row, every tag stays.  An ordinary resident key is updated
+    beside it either way."""
+    rng = np.random.default_rng(77 + int(accumulate) + 2 * int(device_policy))
     rows, dim = 2000, 16
     uvm = float_table(rng, rows, dim, O.F32)
-    per_set = 8 * 8 + 8 * dim * 4 + 8 * 4  # tags, rows, counters (all multiples of 16)
-    ct = CachedTable(uvm, 128 * per_set, 8)
+    per_set = 8 * 8 + 8 * dim * 4 + (8 * 4 if device_policy else 0)  # tags, rows, counters
+    ct = CachedTable(uvm, 128 * per_set, 8, modify_on_gpu=device_policy)
     assert ct.num_sets == 128
     ct.model.insert_keys(np.array([11], np.int64), uvm=ct.uvm_np.reshape(-1))
     ct.load_model()
@@ -302,6 +309,8 @@ def test_update_reaches_every_way_whose_rebuilt_key_matches(accumulate):
     keys = np.array([odd, 11, odd] if accumulate else [odd, 11], np.int64)
     upd = dyadic(rng, (keys.size, dim)).astype(np.float32)
     tags0, _, _, rows0 = cache_state(ct)
+    ways0 = slots_of(tags0, ct.num_sets, odd)
+    assert ways0 == [s * 8 + w for w in range(8)]
     d_keys, d_upd = to_dev(keys), to_dev(upd.view(np.uint8).reshape(-1))
     if accumulate:
         _lib.call("nve_table_update_accumulate", ct.table, ct.ctx, keys.size, vp(d_keys), dim * 4, dim * 4,
@@ -310,17 +319,27 @@ def test_update_reaches_every_way_whose_rebuilt_key_matches(accumulate):
         _lib.call("nve_table_update", ct.table, ct.ctx, keys.size, vp(d_keys), dim * 4, dim * 4, vp(d_upd))
     torch.cuda.synchronize()
     tags1, _, _, rows1 = cache_state(ct)
-    assert np.array_equal(tags1, tags0)
+    own_tag = (odd % (1 << 64)) // ct.num_sets
+    assert own_tag == (1 << 57) - 1
+    exp_tags = tags0.copy()
+    written = ways0 if device_policy else ways0[:1]
+    if device_policy:
+        exp_tags[ways0] = own_tag
+    assert np.array_equal(tags1, exp_tags)
+    # the committed tags still rebuild to the odd key
+    assert slots_of(tags1, ct.num_sets, odd) == ways0
     sl11 = slot_of(tags1, ct.num_sets, 11)
-    ways = slots_of(tags1, ct.num_sets, odd)
-    assert len(ways) == 8 and sl11 not in ways
+    assert sl11 not in ways0
     r11 = rows1[sl11].view(np.float32)
     if accumulate:
         assert np.array_equal(r11, rows0[sl11].view(np.float32) + upd[1])
-        for w in ways:  # both occurrences of the odd key add to every matching way
+        for w in written:  # both occurrences of the odd key add to every recorded way
             assert np.array_equal(rows1[w].view(np.float32), rows0[w].view(np.float32) + upd[0] + upd[2])
     else:
         assert np.array_equal(r11, upd[1])
-        for w in ways:
+        for w in written:
             assert np.array_equal(rows1[w].view(np.float32), upd[0])
+    for w in ways0:
+        if w not in written:
+            assert np.array_equal(rows1[w], rows0[w])
     ct.close()
