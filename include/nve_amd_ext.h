@@ -96,17 +96,24 @@ NVE_C_API nve_status_t nve_amd_dedup_gather(nve_key_type_t key_type, int64_t num
  * nothing: its scratch is a fixed 16 MiB device array, one per GPU, held
  * until the process ends.  num_keys must not exceed 262,144 (larger batches
  * fail with NVE_ERROR_INVALID_ARGUMENT).  Every call on one GPU uses that
- * GPU's array, so calls that overlap on one GPU (two streams, two threads)
- * race and must be serialized by the caller.  Same results as
- * nve_amd_dedup_gather; asynchronous on `stream`. */
+ * GPU's array, so the library runs the calls on one GPU one after another, in
+ * the order they are issued from any thread or stream: each call's stream
+ * waits for the previous call's completion event (one event per GPU, made
+ * with the array's address on the GPU's first call).  Under HIP graph capture
+ * that ordering is not recorded: a replayed graph must not overlap other
+ * calls on its GPU.  Same results as nve_amd_dedup_gather; asynchronous on
+ * `stream`. */
 NVE_C_API nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_keys,
                                                     const void* keys, const void* table,
                                                     int64_t num_rows, int64_t row_size_in_bytes,
                                                     void* output, int64_t output_stride, void* stream);
 
 /* Random-row read microbenchmark: reads row idx[i] (row_size_in_bytes each, a
- * multiple of 16) of a device table for i < n and folds the bytes into sink
- * (one uint32 per 256-thread workgroup, ceil(n/128) words). */
+ * multiple of 16) of a table for i < n and folds the bytes into sink (one
+ * uint32 per 256-thread workgroup, ceil(n/128) words).  The table may be
+ * device memory (the HBM random-row ceiling) or pinned host memory from
+ * hipHostMalloc (the host link's random-row ceiling, which bounds the reads
+ * of missed rows from a LinearUVM backing table). */
 NVE_C_API nve_status_t nve_amd_read_ceiling(const void* table, int64_t row_size_in_bytes,
                                             const int64_t* idx, int64_t n, uint32_t* sink,
                                             void* stream);

@@ -964,10 +964,12 @@ nve_status_t nve_amd_dedup_gather_noalloc(nve_key_type_t key_type, int64_t num_k
   const size_t need = dedup_workspace_bytes(num_keys);
   NVE_CHECK(need <= kNoAllocScratchBytes, "The device scratch (", kNoAllocScratchBytes,
             " bytes) is smaller than the dedup workspace of ", num_keys, " keys (", need, " bytes)");
-  void* ws = nullptr;
-  NVE_HIP(noalloc_scratch(&ws));
+  // the GPU's scratch array, with this call ordered after the previous one
+  NoAllocSession ses;
+  NVE_HIP(ses.begin((hipStream_t)stream));
   dedup_gather_run(key_bytes_of(key_type), num_keys, keys, static_cast<const uint8_t*>(table), num_rows,
-                   row_size_in_bytes, output, output_stride, ws, need, (hipStream_t)stream);
+                   row_size_in_bytes, output, output_stride, ses.device_scratch(), need, (hipStream_t)stream);
+  NVE_HIP(ses.end());
   return NVE_SUCCESS;
   C_CATCH
 }

@@ -63,3 +63,28 @@ def test_rejects_batches_above_the_maximum():
     with pytest.raises(_lib.InvalidArgument):
         _lib.call("nve_amd_dedup_gather_noalloc", _lib.KEY_INT64, keys.numel(), vp(keys), vp(table), 10, 16,
                   vp(out), 16, stream_ptr())
+
+
+def test_calls_on_two_streams_are_ordered():
+    """Two calls issued back to back on two streams, with no synchronization
+    between them, share the GPU's scratch array: the library orders the second
+    after the first, so both match the workspace entry.  Then a third call on
+    the first stream, again without a sync, ordered after the second."""
+    rows, dim = 200_000, 64
+    width = dim * 2
+    g = torch.Generator(device="cuda")
+    g.manual_seed(23)
+    table = torch.randn((rows, dim), device="cuda", generator=g).half()
+    batches = [(torch.randint(0, rows, (n,), device="cuda", generator=g) ** 2 // rows).to(torch.int64)
+               for n in (262144, 200000, 150000)]
+    refs = [with_workspace(k, table, rows, width) for k in batches]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.full((k.numel(), dim), -7.0, dtype=torch.float16, device="cuda") for k in batches]
+    torch.cuda.synchronize()
+    print("[no_alloc] three calls on two streams", flush=True)
+    for k, o, s in zip(batches, outs, (s1, s2, s1)):
+        _lib.call("nve_amd_dedup_gather_noalloc", _lib.KEY_INT64, k.numel(), vp(k), vp(table), rows, width, vp(o),
+                  width, ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        assert torch.equal(o.view(torch.int16), r.view(torch.int16))
