@@ -127,11 +127,14 @@ def quantiles(ts):
     return ts[n // 2], ts[max(0, int(0.1 * n))], ts[min(n - 1, int(0.9 * n))]
 
 
-def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, seconds, what):
+def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, seconds, what, check):
     """The product HostLayer timed on this host's cores on whole batches of the
     workload: the reference's default worker count max(cores - 2, 1)
     (thread_pool.cpp:112-116) for `value`, and every core beside it; median
-    batch time with p10 / p90 (at least 20 batches after 3 warm-up ones)."""
+    batch time with p10 / p90 (at least 20 batches after 3 warm-up ones).
+    After each timing, untimed, one more batch (the first) is run and
+    `check()` compares its output with the CPU oracle's restatement of the
+    reference HostLayer (bit for bit) or raises."""
     model, avail = cpu_info()
     n = key_batches[0].size
     res = {}
@@ -139,12 +142,14 @@ def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, s
         base = HostLayerBaseline(lib, h_table, rows, row_bytes, dtype, threads)
         try:
             ts = time_batches(lambda k: run_batch(base, k), key_batches, seconds)
+            run_batch(base, key_batches[0])
+            checked = check()
         finally:
             base.close()
         med, p10, p90 = quantiles(ts)
         res[label] = {"threads": threads, "batches": len(ts), "median_ms": round(med * 1e3, 3),
                       "p10_ms": round(p10 * 1e3, 3), "p90_ms": round(p90 * 1e3, 3),
-                      "lookups_per_s": round(n / med, 1)}
+                      "lookups_per_s": round(n / med, 1), "checked": checked}
         log(f"cpu baseline ({label}, {threads} threads): median {med * 1e3:.2f} ms per {n}-key batch "
             f"(p10 {p10 * 1e3:.2f}, p90 {p90 * 1e3:.2f}) = {n / med / 1e6:.1f} M lookups/s")
     d = res["default"]
@@ -152,7 +157,28 @@ def cpu_baseline(lib, h_table, rows, row_bytes, dtype, key_batches, run_batch, s
             "sample": f"{d['batches']} whole batches of {n} keys ({what}), median batch time, on '{model}' "
                       f"({avail} cores available): the product HostLayer (libnve_amd.so, CPU threads)",
             "median_ms": d["median_ms"], "p10_ms": d["p10_ms"], "p90_ms": d["p90_ms"],
-            "all_cores": res["all_cores"]}
+            "checked": d["checked"], "all_cores": res["all_cores"]}
+
+
+def host_pool_check(h_table, row_bytes, dtype, keys, out, bags, hot):
+    """A check for cpu_baseline: `out` (the HostLayer's Fixed-hotness Sum of
+    `keys`) equals the oracle's reference HostLayer order (cpu_pooling.hpp:
+    68-150) bit for bit.  The oracle is the checker here, not the thing timed."""
+    import numpy as np
+    from oracle import oracle as O
+    from pynve import _lib
+
+    odt = O.F16 if out.dtype == np.float16 else O.F32
+    rdt = O.F16 if dtype == _lib.DT_F16 else O.F32
+    count = out.shape[1]
+
+    def check():
+        ref = O.pool(O.linear_row_ptrs(keys, h_table, row_bytes), rdt, count, O.FIXED, O.SUM, keys.size, None,
+                     bags, hot, None, 0, odt, host_order=True)
+        if not np.array_equal(out.view(ref.dtype), ref):
+            raise SystemExit("bench.py: the CPU HostLayer's output differs from the oracle's reference order")
+        return f"all {bags} bags of the first batch bit-exact with the oracle's HostLayer order"
+    return check
 
 
 def read_ceiling(torch, lib, stream, counts):
@@ -195,6 +221,41 @@ def read_ceiling(torch, lib, stream, counts):
     return res
 
 
+def host_link_ceiling(torch, lib, stream, host_ptr, rows, row_bytes, counts, reps=20):
+    """The same plain row-read kernel (nve_amd_read_ceiling) on uniform random
+    rows of a pinned host table (hipHostMalloc, read by the GPU over the host
+    link): the host link's random-row read rate.  Returns
+    {rows_per_launch: (GB/s, us per launch)}; bytes counted are the rows and
+    their 8-byte indices."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    s = ctypes.c_void_p(stream.cuda_stream)
+    fn = lib.load().nve_amd_read_ceiling
+    res = {}
+    for n in counts:
+        idx = torch.randint(0, rows, (n,), device="cuda", generator=gen, dtype=torch.int64)
+        sink = torch.zeros((n + 127) // 128, dtype=torch.int32, device="cuda")
+        args = (ctypes.c_void_p(host_ptr), row_bytes, ctypes.c_void_p(idx.data_ptr()), n,
+                ctypes.c_void_p(sink.data_ptr()), s)
+
+        def launch():
+            st = fn(*args)
+            if st:
+                lib.check(st)
+
+        for _ in range(3):
+            launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[n] = ((n * row_bytes + n * 8) / (ms * 1e-3) / 1e9, ms * 1e3)
+    return res
+
+
 def step_spread(torch, stream, step, groups=20, per_group=10):
     """Spread of the step time: `groups` runs of `per_group` back-to-back steps,
     each bracketed by events on `stream` (an event between every single step
@@ -222,18 +283,19 @@ def f16_ulp(torch, x):
     return torch.clamp(torch.ldexp(torch.ones_like(x), (e - 11).to(torch.int32)), min=2.0 ** -24)
 
 
-def check_pooled_bags(torch, table, keys, out, hot, bag_ids):
-    """Untimed check of sampled bags of a Fixed-hotness Sum lookup against
+def check_pooled_bags(torch, table, keys, out, hot):
+    """Untimed check of every bag of a Fixed-hotness Sum lookup against
     torch's own gather summed in float64: each fp16 output within one fp16
     ulp of the exact sum, or within 1e-5 of the row's largest magnitude."""
-    for b in bag_ids:
-        ref = table[keys[b * hot:(b + 1) * hot]].double().sum(0)
-        got = out[b].double()
-        tol = f16_ulp(torch, ref.half().double()) + 1e-5 * ref.abs().max()
-        bad = int(((got - ref).abs() > tol).sum().item())
-        if bad:
-            raise SystemExit(f"bench.py: pooled bag {b} differs from its float64 sum in {bad} elements")
-    return len(bag_ids)
+    bags = out.shape[0]
+    ref = table[keys].double().view(bags, hot, -1).sum(1)
+    got = out.double()
+    tol = f16_ulp(torch, ref.half().double()) + 1e-5 * ref.abs().amax(1, keepdim=True)
+    bad = ((got - ref).abs() > tol).sum(1)
+    if int(bad.sum().item()):
+        first = int(torch.nonzero(bad)[0].item())
+        raise SystemExit(f"bench.py: pooled bag {first} differs from its float64 sum in {int(bad[first])} elements")
+    return bags
 
 
 def host_call_costs(torch, lib, calls=400):
@@ -439,7 +501,8 @@ def run_workload(args, torch, _lib):
             extra["cpu_baseline"] = cpu_baseline(
                 _lib, h_table, rows, width, _lib.DT_F32, h_keys,
                 lambda base, k: base.pooled(k, h_pooled, width, hot, _lib.DT_F32), args.cpu_seconds,
-                f"Fixed {hot} x {bags} bags, Sum, fp32")
+                f"Fixed {hot} x {bags} bags, Sum, fp32",
+                host_pool_check(h_table, width, _lib.DT_F32, h_keys[0], h_pooled, bags, hot))
             gb = HostLayerBaseline(_lib, h_table, rows, width, _lib.DT_F32, max(cpu_info()[1] - 2, 1))
             try:
                 ts = time_batches(lambda k: gb.gather(k, h_gathered, width), h_keys, args.cpu_seconds / 2)
@@ -590,17 +653,34 @@ def run_workload(args, torch, _lib):
         layer, ctx = ctypes.c_void_p(), ctypes.c_void_p()
         _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), table, None)
         _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(ctx), sp, sp, None, None)
-        if args.c3_prefill:
-            # every row of the backing table into the cache first (the table must fit it), so
-            # that the lookups measure the cache-hit path alone
-            tctx = ctypes.c_void_p()
-            _lib.call("nve_table_create_execution_context", table, ctypes.byref(tctx), sp, sp, None, None)
-            step = 1 << 20
-            for r0 in range(0, rows, step):
-                ks = torch.arange(r0, min(rows, r0 + step), dtype=torch.int64, device="cuda")
-                _lib.call("nve_amd_table_insert_from_uvm", table, tctx, ks.numel(), ctypes.c_void_p(ks.data_ptr()))
-                _lib.call("nve_context_wait", tctx)
-            _lib.call("nve_context_destroy", tctx)
+        if args.c3_resident:
+            # every row of the backing table resident in the cache, loaded as a cache
+            # state (tags and rows written through import_state and the data pointer,
+            # as a checkpoint restore would), so that the lookups measure the
+            # cache-hit path alone: key k sits in set k % num_sets, way k // num_sets
+            ns_ = ctypes.c_int64()
+            _lib.call("nve_amd_gpu_table_num_sets", table, ctypes.byref(ns_))
+            ns = ns_.value
+            if rows > 8 * ns:
+                raise SystemExit(f"c3: --c3-resident needs rows <= 8 * num_sets ({8 * ns})")
+            idx = torch.arange(rows, dtype=torch.int64, device="cuda")
+            slot = (idx % ns) * 8 + idx // ns
+            tags = torch.full((ns * 8,), -1, dtype=torch.int64, device="cuda")
+            tags[slot] = idx // ns
+            data = torch.zeros((ns * 8, dim), dtype=torch.float16, device="cuda")
+            for r0 in range(0, rows, 1 << 22):
+                r1 = min(rows, r0 + (1 << 22))
+                part = torch.empty((r1 - r0, dim), dtype=torch.float16, device="cuda")
+                assert hip.hipMemcpy(part.data_ptr(), host_ptr.value + r0 * width, (r1 - r0) * width, 1) == 0
+                data[slot[r0:r1]] = part
+            torch.cuda.synchronize()
+            dptr = ctypes.c_void_p()
+            _lib.call("nve_amd_gpu_table_data", table, ctypes.byref(dptr))
+            assert hip.hipMemcpy(dptr.value, data.data_ptr(), data.numel() * 2, 3) == 0
+            _lib.call("nve_amd_gpu_table_import_state", table, ctypes.c_void_p(tags.data_ptr()), None, None, 0)
+            torch.cuda.synchronize()
+            del idx, slot, tags, data
+            torch.cuda.empty_cache()
         concat = args.c3_concat
         out = torch.empty((nkeys if concat else bags, dim), dtype=torch.float16, device="cuda")
         hr = (ctypes.c_float * 1)()
@@ -638,8 +718,34 @@ def run_workload(args, torch, _lib):
         ms = e0.elapsed_time(e1) / args.steps
         hit = sum(rates) / len(rates)
         log(f"c3: {ms * 1000:.1f} us/step (events), {wall * 1000:.1f} us/step (wall), mean hit rate {hit:.4f}")
+        ms_events = ms
         ms = max(ms, wall)  # the step includes a host sync (hit rate) and any insert
-        if args.c3_insert_steps > 0 and not args.c3_prefill:
+        if not args.c3_resident:
+            # the host link's random-row read ceiling: the plain read kernel on uniform
+            # rows of this same pinned table (far larger than any cache on the way), at
+            # about one batch's misses, one batch and four batches of rows per launch
+            miss_rows = max(1, int(nkeys * (1 - hit)))
+            hl = host_link_ceiling(torch, _lib, stream, host_ptr.value, rows, width,
+                                   [miss_rows, nkeys, 4 * nkeys])
+            for n_, (g_, us_) in hl.items():
+                log(f"c3: host-link random-row read kernel: {g_:.1f} GB/s at {n_} rows/launch ({us_:.1f} us)")
+            ceiling = max(g for g, _ in hl.values())
+            miss_bytes = miss_rows * width
+            # the misses' rate over the step's device time (hits, tags and the
+            # hit-rate readback included, so a lower bound on the miss path's rate)
+            miss_rate = miss_bytes / (ms_events * 1e-3) / 1e9
+            extra["host_link"] = {
+                "ceiling_GBps": round(ceiling, 2),
+                "read_kernel": {str(n_): {"GBps": round(g_, 2), "us": round(us_, 2)} for n_, (g_, us_) in hl.items()},
+                "miss_bytes_per_step": miss_bytes,
+                "miss_GBps_over_step": round(miss_rate, 2),
+                "frac_of_ceiling": round(miss_rate / ceiling, 4),
+                "note": "read kernel = nve_amd_read_ceiling over uniform random 256 B rows of the same "
+                        "hipHostMalloc table; the miss rate divides the missed rows' bytes by the whole "
+                        "lookup step's device time (events)"}
+            log(f"c3: misses {miss_bytes / 1e6:.2f} MB per step at {miss_rate:.1f} GB/s over the step = "
+                f"{miss_rate / ceiling:.3f} of the host link's {ceiling:.1f} GB/s read ceiling")
+        if args.c3_insert_steps > 0 and not args.c3_resident:
             # the insert behind auto-insert, timed on its own: histogram of a whole
             # batch, replacement, rows copied from the host table (the reference's
             # GpuTable::insert path, gpu_table.cu:579-1046), each call waited for
@@ -660,7 +766,7 @@ def run_workload(args, torch, _lib):
             cfg_out["insert_us"] = {"median": round(ins[len(ins) // 2], 1), "min": round(ins[0], 1),
                                     "max": round(ins[-1], 1), "calls": len(ins), "keys_per_call": nkeys}
             log(f"c3: insert of a {nkeys}-key batch: median {ins[len(ins) // 2]:.1f} us over {len(ins)} calls")
-        if args.c3_update_steps > 0:
+        if args.c3_update_steps > 0 and not args.c3_resident:
             # the cache's update and update_accumulate of a whole batch (every key
             # resident) on a cache-only table of the same rows (4 GiB, no backing
             # table to write through to): records of the ways, invalidate, order
@@ -709,7 +815,7 @@ def run_workload(args, torch, _lib):
                         "zipf_alpha": alpha, "mean_hit_rate": round(hit, 4),
                         "host_link_bytes_per_step": int(nkeys * (1 - hit)) * width,
                         "lookup": "concat" if concat else f"pooled {bags} x {hot} Sum",
-                        "kernel_mode": args.kernel_mode, "prefilled": bool(args.c3_prefill),
+                        "kernel_mode": args.kernel_mode, "resident": bool(args.c3_resident),
                         "host_pages_touched": not args.c3_no_touch,
                         "step": "lookup + hit-rate readback + auto-insert when the heuristic fires"})
         _lib.call("nve_context_destroy", ctx)
@@ -876,7 +982,10 @@ def main():
     ap.add_argument("--c3-insert-steps", type=int, default=5,
                     help="c3: time this many whole-batch inserts from the backing table after the lookups")
     ap.add_argument("--c3-prefill", action="store_true",
-                    help="c3: insert every backing row into the cache before the lookups (hit path only)")
+                    help="c3: disabled (see --c3-resident)")
+    ap.add_argument("--c3-resident", action="store_true",
+                    help="c3: every backing row resident in the cache (loaded as a cache state) before the "
+                         "lookups: the hit path alone; no inserts or updates are timed")
     ap.add_argument("--kernel-mode", type=int, default=0, choices=[0, 1, 2, 3],
                     help="c3: GPU table lookup mode (0 auto, 1 LookupUVM, 2 SortGather, 3 PipelineGather)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -887,6 +996,12 @@ def main():
                     help="only run torch's device copy of a 1 GiB buffer 5 times (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
+    if args.c3_prefill:
+        # a run of this mode (insert_from_uvm of 2^20 distinct keys into a 4 GiB
+        # cache, then the lookups and the update timings) faulted the GPU and its
+        # cause is not found: the mode stays off; --c3-resident measures the hit path
+        raise SystemExit("bench.py: --c3-prefill is disabled (it faulted the GPU, cause not found); "
+                         "use --c3-resident")
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the lookup path is single-GPU; across GPUs "
@@ -975,9 +1090,8 @@ def main():
     spread = step_spread(torch, stream, step)
     step(0)
     torch.cuda.synchronize()
-    checked = check_pooled_bags(torch, d_table, batches[0], out, hot,
-                                sorted({0, 1, bags // 2, bags - 1, 7 % bags, (bags * 3) // 4}))
-    log(f"step spread {spread}; {checked} sampled bags match their float64 sums")
+    checked = check_pooled_bags(torch, d_table, batches[0], out, hot)
+    log(f"step spread {spread}; all {checked} bags match their float64 sums")
 
     # algorithmic bytes per launch: keys + one stored row per key + pooled output
     alg = nkeys * 8 + nkeys * width + bags * width
@@ -1030,7 +1144,9 @@ def main():
             base.pooled(k, h_out, width, hot, _lib.DT_F16)
 
         result["cpu_baseline"] = cpu_baseline(_lib, h_table, rows, width, _lib.DT_F16, h_keys, run_batch,
-                                              args.cpu_seconds, f"Fixed {hot} x {bags} bags, Sum, fp16")
+                                              args.cpu_seconds, f"Fixed {hot} x {bags} bags, Sum, fp16",
+                                              host_pool_check(h_table, width, _lib.DT_F16, h_keys[0], h_out,
+                                                              bags, hot))
         del h_table
     _lib.call("nve_context_wait", ctx)
     _lib.call("nve_context_destroy", ctx)

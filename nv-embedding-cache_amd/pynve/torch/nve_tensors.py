@@ -1,9 +1,15 @@
-"""CachedTable: the `weight` Parameter of the NVEmbedding layers
-(python/pynve/torch/nve_tensors.py:18-80).
+"""CachedTable: the `weight` Parameter of the NVEmbedding layers (the role of
+the reference's python/pynve/torch/nve_tensors.py:18-80).
 
-It wraps the table's storage and keeps a reference to the layer binding
-(`emb_layer`).  `add_` is the optimizer's update hook: a sparse row-gradient
-is accumulated into the layer's table and caches (nve_tensors.py:64-80).
+The parameter's data is the layer's table as torch sees it; the native layer
+binding that owns the table and its caches rides along as `emb_layer`.  Two
+things differ from a plain Parameter:
+
+* the binding is a process-local native handle, so it is left out of the
+  pickled state (torch.export.save pickles the module's parameters; the
+  exported graph reaches the layer through its marker tensor instead);
+* `add_` is the optimizer's update hook: a sparse row gradient is sent to the
+  layer's accumulate, which updates the table and every cache holding a row.
 """
 import torch
 
@@ -11,19 +17,22 @@ from .. import _lib
 
 
 class CachedTable(torch.nn.parameter.Parameter):
-    def __new__(cls, *args, **kwargs):
-        if "cache" not in kwargs:
-            raise Exception("building a CachedTable Tensor require a viable cache argument")
-        cache = kwargs.pop("cache")
-        instance = super().__new__(cls, *args, **kwargs)
-        instance.emb_layer = cache
-        return instance
+    # attributes that only mean something inside this process
+    _PROCESS_LOCAL = ("emb_layer",)
+
+    def __new__(cls, data=None, requires_grad=True, *, cache):
+        # `cache` is keyword-only and has no default: a CachedTable without a
+        # layer binding behind it cannot apply an update, so there is none
+        if cache is None:
+            raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT,
+                                       "CachedTable needs the layer binding that owns the table (cache=)")
+        param = super().__new__(cls, data, requires_grad)
+        param.emb_layer = cache
+        return param
 
     def __getstate__(self):
-        # the binding holds native handles and cannot be pickled
-        state = dict(self.__dict__)
-        state["emb_layer"] = None
-        return state
+        # a copy: the live parameter keeps its binding after being pickled
+        return {k: (None if k in self._PROCESS_LOCAL else v) for k, v in self.__dict__.items()}
 
     def add_(self, other, *, alpha=1):
         """self += alpha * other for a sparse `other` over rows (its nonzero

@@ -132,3 +132,33 @@ def test_user_memblock():
     assert mb.get_type() == nve.MemBlockType.User
     assert mb.get_ptr() == 0x1000 and mb.get_size_in_bytes() == 64
     assert nve.dtype_size(nve.DataType_t.Float16) == 2
+
+
+def test_cached_table_binding_is_required_and_stays_out_of_pickles():
+    import io
+    import pickle
+
+    from pynve.torch.nve_tensors import CachedTable
+
+    class Binding:  # stands for a native layer binding: not picklable
+        def __reduce__(self):
+            raise TypeError("native handle")
+
+    with pytest.raises(TypeError):
+        CachedTable(torch.zeros(2, 3))  # cache= is a required keyword
+    with pytest.raises(_lib.InvalidArgument):
+        CachedTable(torch.zeros(2, 3), cache=None)
+    b = Binding()
+    w = CachedTable(torch.arange(6.0).reshape(2, 3), cache=b)
+    assert isinstance(w, torch.nn.Parameter) and w.requires_grad and w.emb_layer is b
+    assert w.__getstate__()["emb_layer"] is None
+    buf = io.BytesIO()
+    torch.save({"w": w}, buf)  # would raise if the binding were pickled
+    assert w.emb_layer is b  # the live parameter keeps its binding
+    buf.seek(0)
+    back = torch.load(buf, weights_only=False)["w"]  # written by this test itself
+    assert torch.equal(back.detach(), w.detach())
+    with pytest.raises(TypeError):
+        pickle.dumps(b)
+    with pytest.raises(_lib.InvalidArgument):
+        w.add_(torch.ones(2, 3))  # dense updates are not row updates
