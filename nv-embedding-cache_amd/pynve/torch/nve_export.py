@@ -6,7 +6,8 @@ A save directory holds, as the reference writes it (nve_export.py:16-40):
                                 {"remote_ps": {}, "memblocks": {key: descriptor}},
                                 "layers": [per-layer entry, ...]}
     save_dir/weights/<key>.nve  one .nve table file per storage resource
-    save_dir/model.pt2          torch.export program (export only)
+    save_dir/model.pt2          torch.export program (export) or AOTInductor
+                                package (export_aot)
 
 A memory-block descriptor is {"type", "row_elements", "num_rows", "dtype"};
 a layer entry is {"id", "module_path", "num_embeddings", "embedding_size",
@@ -178,26 +179,69 @@ def export(model, example_inputs, save_dir, *, dynamic_shapes=None, ps_data_path
     torch.export.save(exported, os.path.join(save_dir, "model.pt2"))
 
 
+# The package must keep each layer's marker as a constant that can be replaced
+# after loading (AOTInductor otherwise folds a buffer into the compiled code and
+# leaves nothing to point at the rebuilt layer): runtime constant folding keeps
+# constants in the package's constant table.
+_AOT_KEEP_CONSTANTS = {"aot_inductor.use_runtime_constant_folding": True}
+
+
 def export_aot(model, example_inputs, save_dir, *, dynamic_shapes=None, inductor_configs=None,
                ps_data_paths=None):
-    """AOTInductor packaging (nve_export.py:321-360): not in this build -- the
-    ops are registered from Python, which an AOTI package run outside Python
-    cannot call.  Use `export` / `load`."""
-    raise _lib.NotImplementedInBuild(_lib.NOT_IMPLEMENTED,
-                                     "export_aot (AOTInductor packages) is not part of this build; "
-                                     "use export() / load()")
+    """save_nve plus an AOTInductor package of `model` as model.pt2
+    (nve_export.py:321-360), loadable by `load_aot` here or by a C++ host
+    through torch::inductor::AOTIModelPackageLoader and nve::LayerDirectory
+    (include/nve_loader.hpp).  `inductor_configs` entries override the
+    defaults, the constant-folding switch included (a package built without it
+    cannot be pointed at new layers)."""
+    _require_torch_ops("export_aot")
+    save_nve(model, save_dir, ps_data_paths=ps_data_paths)
+    configs = {**_AOT_KEEP_CONSTANTS, **(inductor_configs or {})}
+    program = torch.export.export(model, example_inputs, dynamic_shapes=dynamic_shapes)
+    torch._inductor.aoti_compile_and_package(program, package_path=os.path.join(save_dir, "model.pt2"),
+                                             inductor_configs=configs)
+
+
+def _device_index(device):
+    if device is None:
+        return torch.cuda.current_device()
+    device = torch.device(device)
+    if device.type == "cpu":
+        return -1
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def load_aot(save_dir, *, gpu_cache_size_override=None, device=None):
-    raise _lib.NotImplementedInBuild(_lib.NOT_IMPLEMENTED,
-                                     "load_aot (AOTInductor packages) is not part of this build; "
-                                     "use export() / load()")
+    """(loader, layers) of an `export_aot` directory (nve_export.py:741-800):
+    the layers rebuilt with their weights, and an AOTIModelPackageLoader whose
+    marker constants are the new layers' markers, so `loader.run(inputs)`
+    reaches them.  The loader holds the markers without owning them: keep
+    `layers` alive while the loader runs."""
+    _require_torch_ops("load_aot")
+    from torch._C._aoti import AOTIModelPackageLoader
+
+    index = _device_index(device)
+    layers = load_nve_layers(save_dir, gpu_cache_size_override=gpu_cache_size_override,
+                             device=torch.device("cpu") if index < 0 else torch.device("cuda", index))
+    loader = AOTIModelPackageLoader(os.path.join(save_dir, "model.pt2"), "model", False, 1, index)
+    rebind_markers(loader, layers)
+    return loader, layers
 
 
 def rebind_markers(loader, layers):
-    raise _lib.NotImplementedInBuild(_lib.NOT_IMPLEMENTED,
-                                     "rebind_markers applies to AOTInductor loaders, which are not "
-                                     "part of this build")
+    """Point each layer's marker constant of `loader` at the layer's
+    marker_tensor, in both of the package's constant buffers and without a
+    copy (nve_export.py:801; idempotent).  load_aot calls it; call it again
+    after the package's constants were replaced (a constant-buffer swap copies
+    the markers, and the ops know only the registered tensors)."""
+    known = set(loader.get_constant_fqns())
+    for layer in layers:
+        fqn = _marker_fqn(layer._export_module_path)
+        if fqn not in known:
+            raise RuntimeError(f"the package has no replaceable constant '{fqn}' (it holds {sorted(known)}): "
+                               "it was not built by export_aot, which keeps runtime constant folding on")
+        for inactive in (False, True):
+            loader.load_constants({fqn: layer.marker_tensor}, inactive, False, True)
 
 
 def _build_ps_from_config(ps_config):

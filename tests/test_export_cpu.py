@@ -87,8 +87,55 @@ def test_device_and_reference_errors(tmp_path):
         E.load_nve_layers(d, device=torch.device("cpu"))
 
 
-def test_aot_entry_points_say_not_in_build():
-    with pytest.raises(_lib.NotImplementedInBuild):
-        E.export_aot(None, (), "/nonexistent")
-    with pytest.raises(_lib.NotImplementedInBuild):
-        E.load_aot("/nonexistent")
+class _FakeLoader:
+    """The two methods of AOTIModelPackageLoader that rebind_markers uses."""
+
+    def __init__(self, fqns):
+        self.fqns, self.calls = list(fqns), []
+
+    def get_constant_fqns(self):
+        return self.fqns
+
+    def load_constants(self, mapping, use_inactive, check_full_update, user_managed):
+        self.calls.append((dict(mapping), use_inactive, check_full_update, user_managed))
+
+
+class _Layer:
+    def __init__(self, path, marker):
+        self._export_module_path, self.marker_tensor = path, marker
+
+
+def test_rebind_markers_points_both_buffers_at_the_live_markers():
+    m1, m2 = torch.tensor([7]), torch.tensor([9])
+    layers = [_Layer("", m1), _Layer("tower.bag", m2)]
+    fake = _FakeLoader(["marker_tensor", "tower.bag.marker_tensor", "dense.weight"])
+    E.rebind_markers(fake, layers)
+    # each marker, no copy, into the active and the inactive buffer, user-managed
+    assert [(list(c[0]), c[1], c[2], c[3]) for c in fake.calls] == [
+        (["marker_tensor"], False, False, True), (["marker_tensor"], True, False, True),
+        (["tower.bag.marker_tensor"], False, False, True), (["tower.bag.marker_tensor"], True, False, True)]
+    assert fake.calls[0][0]["marker_tensor"] is m1 and fake.calls[3][0]["tower.bag.marker_tensor"] is m2
+    # a package whose marker was folded away cannot be rebound
+    with pytest.raises(RuntimeError, match="no replaceable constant 'tower.bag.marker_tensor'"):
+        E.rebind_markers(_FakeLoader(["marker_tensor"]), layers)
+
+
+def test_export_aot_keeps_markers_replaceable(tmp_path, monkeypatch):
+    """export_aot turns runtime constant folding on unless the caller says
+    otherwise, and packages the exported program as save_dir/model.pt2."""
+    seen = {}
+    monkeypatch.setattr(E, "save_nve", lambda model, save_dir, ps_data_paths=None: seen.setdefault("saved", save_dir))
+    monkeypatch.setattr(E, "HAS_TORCH_OPS", True)
+    monkeypatch.setattr(E, "_require_torch_ops", lambda name: None)
+    monkeypatch.setattr(torch.export, "export", lambda m, a, dynamic_shapes=None: ("program", m, a, dynamic_shapes))
+    monkeypatch.setattr(torch._inductor, "aoti_compile_and_package",
+                        lambda prog, package_path, inductor_configs: seen.update(
+                            prog=prog, path=package_path, cfg=inductor_configs))
+    model = object()
+    E.export_aot(model, (1,), str(tmp_path))
+    assert seen["saved"] == str(tmp_path) and seen["path"] == os.path.join(str(tmp_path), "model.pt2")
+    assert seen["prog"] == ("program", model, (1,), None)
+    assert seen["cfg"] == {"aot_inductor.use_runtime_constant_folding": True}
+    E.export_aot(model, (1,), str(tmp_path), inductor_configs={"max_autotune": True,
+                                                              "aot_inductor.use_runtime_constant_folding": False})
+    assert seen["cfg"] == {"max_autotune": True, "aot_inductor.use_runtime_constant_folding": False}
