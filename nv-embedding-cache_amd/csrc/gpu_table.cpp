@@ -47,7 +47,6 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   num_sets_ = cfg_.cache_size / per_set;
   NVE_CHECK(num_sets_ > 0, "Memory allocated to the cache is too small");
   NVE_CHECK(num_sets_ <= UINT32_MAX, "Too many cache sets");
-  div_ = make_set_divisor(num_sets_);
   const uint64_t ways = num_sets_ * kWays;
   const size_t data_bytes = (size_t)ways * (size_t)cfg_.row_size_in_bytes;
   NVE_LOG_INFO("GpuTable on device ", cfg_.device_id, ": ", num_sets_, " sets of 8 ways, ",
@@ -97,7 +96,6 @@ RowSource GpuTable::row_source(bool with_uvm) const {
   s.cache_data = data_;
   s.cache_tags = tags_;
   s.num_sets = num_sets_;
-  s.div = div_;
   return s;
 }
 

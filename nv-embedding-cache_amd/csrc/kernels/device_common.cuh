@@ -430,9 +430,8 @@ __device__ __forceinline__ int64_t unflip_key(uint64_t f, int key_bytes) {
 // ec_set_associative.h:104-112, ec_set_associative.cuh:46-80): 8 tags per set
 // at tags + set*8, rows at data + (set*8 + way)*row_bytes;
 // set = (unsigned)key % num_sets; a hit is the lowest way whose rebuilt key
-// tag*num_sets + set equals the key (both computed without a divide or a
-// multiply per way, set_divisor.hpp); a miss resolves to table +
-// key*row_bytes, or to nothing when table is null.
+// tag*num_sets + set equals the key; a miss resolves to table + key*row_bytes,
+// or to nothing when table is null.
 // Returns the row address (0 when unresolved); *hit reports a cache hit or a
 // linear-table row; *miss a cache miss (whether or not a backing row exists).
 __device__ __forceinline__ uint64_t resolve_row(const RowSource& src, int key_bytes, int64_t key,
@@ -447,30 +446,29 @@ __device__ __forceinline__ uint64_t resolve_row(const RowSource& src, int key_by
   uint32_t mask = 0;
   if (key_bytes == 4) {
     const uint32_t uk = (uint32_t)(int32_t)key;
-    const uint32_t q = set_div32(src.div, uk);
-    set = uk - q * src.div.d;
+    const uint32_t ns = (uint32_t)src.num_sets;
+    set = uk % ns;
     const uint4* tp = reinterpret_cast<const uint4*>(
         reinterpret_cast<const int32_t*>(src.cache_tags) + (uint64_t)set * 8);
     const uint4 t0 = tp[0];
     const uint4 t1 = tp[1];
     const uint32_t t[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
 #pragma unroll
-    for (int w = 0; w < 8; ++w) mask |= (uint32_t)tag_matches32(src.div, t[w], q) << w;
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * ns + set == uk) << w;
   } else {
     const uint64_t uk = (uint64_t)key;
-    const uint64_t q = set_div64(src.div, uk);
-    set = (uint32_t)(uk - q * src.div.d);
+    set = (uint32_t)(uk % src.num_sets);
     const uint4* tp = reinterpret_cast<const uint4*>(
         reinterpret_cast<const int64_t*>(src.cache_tags) + (uint64_t)set * 8);
     uint64_t t[8];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint4 qv = tp[c];
-      t[2 * c] = (uint64_t)qv.x | ((uint64_t)qv.y << 32);
-      t[2 * c + 1] = (uint64_t)qv.z | ((uint64_t)qv.w << 32);
+      const uint4 q = tp[c];
+      t[2 * c] = (uint64_t)q.x | ((uint64_t)q.y << 32);
+      t[2 * c + 1] = (uint64_t)q.z | ((uint64_t)q.w << 32);
     }
 #pragma unroll
-    for (int w = 0; w < 8; ++w) mask |= (uint32_t)tag_matches64(src.div, t[w], q) << w;
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * src.num_sets + set == uk) << w;
   }
   if (mask) {
     const uint32_t way = (uint32_t)__builtin_ctz(mask);

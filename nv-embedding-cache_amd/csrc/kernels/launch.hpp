@@ -9,8 +9,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "set_divisor.hpp"
-
 namespace nve_amd {
 
 constexpr int kMaxPoolTables = 64;  // tables one multi-table pooling launch can address
@@ -23,7 +21,6 @@ struct RowSource {
   const uint8_t* cache_data; // null: no cache
   const void* cache_tags;    // num_sets*8 tags of the key type
   uint64_t num_sets;
-  SetDivisor div;            // division by num_sets without a divide (set_divisor.hpp)
   uint64_t num_rows;         // rows of `table`: keys >= num_rows read nothing (0 = no bound)
 };
 

@@ -131,7 +131,7 @@ struct SplitArgs {
 struct SplitCacheArgs : SplitArgs {
   const uint8_t* cache_data;
   const void* cache_tags;
-  SetDivisor div;                    // division by the number of sets
+  uint64_t num_sets;
   unsigned long long* miss_counter;  // optional, kMissStripes * kMissStripeWords words
 };
 
@@ -146,30 +146,29 @@ __device__ __forceinline__ uint32_t cache_code(const A& a, int64_t key, bool* mi
   uint32_t set, mask = 0;
   if (a.key_bytes == 4) {
     const uint32_t uk = (uint32_t)(int32_t)key;
-    const uint32_t q = set_div32(a.div, uk);
-    set = uk - q * a.div.d;
+    const uint32_t ns = (uint32_t)a.num_sets;
+    set = uk % ns;
     const uint4* tp = reinterpret_cast<const uint4*>(reinterpret_cast<const int32_t*>(a.cache_tags) +
                                                      (uint64_t)set * 8);
     const uint4 t0 = tp[0];
     const uint4 t1 = tp[1];
     const uint32_t t[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
 #pragma unroll
-    for (int w = 0; w < 8; ++w) mask |= (uint32_t)tag_matches32(a.div, t[w], q) << w;
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * ns + set == uk) << w;
   } else {
     const uint64_t uk = (uint64_t)key;
-    const uint64_t q = set_div64(a.div, uk);
-    set = (uint32_t)(uk - q * a.div.d);
+    set = (uint32_t)(uk % a.num_sets);
     const uint4* tp = reinterpret_cast<const uint4*>(reinterpret_cast<const int64_t*>(a.cache_tags) +
                                                      (uint64_t)set * 8);
     uint64_t t[8];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint4 qv = tp[c];
-      t[2 * c] = (uint64_t)qv.x | ((uint64_t)qv.y << 32);
-      t[2 * c + 1] = (uint64_t)qv.z | ((uint64_t)qv.w << 32);
+      const uint4 q = tp[c];
+      t[2 * c] = (uint64_t)q.x | ((uint64_t)q.y << 32);
+      t[2 * c + 1] = (uint64_t)q.z | ((uint64_t)q.w << 32);
     }
 #pragma unroll
-    for (int w = 0; w < 8; ++w) mask |= (uint32_t)tag_matches64(a.div, t[w], q) << w;
+    for (int w = 0; w < 8; ++w) mask |= (uint32_t)(t[w] * a.num_sets + set == uk) << w;
   }
   *miss = mask == 0;
   if (mask) return set * 8u + (uint32_t)__builtin_ctz(mask);
@@ -369,7 +368,7 @@ hipError_t launch_split_g(const PoolLaunch& a, const PoolGeometry& g, hipStream_
     static_cast<SplitArgs&>(c) = s;
     c.cache_data = a.src.cache_data;
     c.cache_tags = a.src.cache_tags;
-    c.div = a.src.div;
+    c.num_sets = a.src.num_sets;
     c.miss_counter = a.miss_counter;
     if (a.weighted)
       hipLaunchKernelGGL((pool_split_kernel<SDT, G, true, true>), grid, block, g.lds_bytes, stream, c);

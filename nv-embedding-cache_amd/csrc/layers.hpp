@@ -219,7 +219,6 @@ class GpuTable {
   int key_bytes_;
   GPUTableConfig cfg_;
   uint64_t num_sets_ = 0;
-  SetDivisor div_{};  // constants of division by num_sets_
   uint8_t* data_ = nullptr;
   void* tags_ = nullptr;
   float* counters_ = nullptr;
