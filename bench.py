@@ -663,10 +663,16 @@ def run_workload(args, torch, _lib):
             ns = ns_.value
             if rows > 8 * ns:
                 raise SystemExit(f"c3: --c3-resident needs rows <= 8 * num_sets ({8 * ns})")
+            # resident keys: row r as key r + offset (--c3-key-offset: keys of more
+            # than 32 bits, as hashed ids are), in set key % num_sets; the
+            # offset is a multiple of num_sets, so rows keep their set and way
+            off = args.c3_key_offset // ns * ns
             idx = torch.arange(rows, dtype=torch.int64, device="cuda")
             slot = (idx % ns) * 8 + idx // ns
             tags = torch.full((ns * 8,), -1, dtype=torch.int64, device="cuda")
-            tags[slot] = idx // ns
+            tags[slot] = (idx + off) // ns
+            if off:
+                batches = [b + off for b in batches]
             data = torch.zeros((ns * 8, dim), dtype=torch.float16, device="cuda")
             for r0 in range(0, rows, 1 << 22):
                 r1 = min(rows, r0 + (1 << 22))
@@ -983,6 +989,9 @@ def main():
                     help="c3: time this many whole-batch inserts from the backing table after the lookups")
     ap.add_argument("--c3-prefill", action="store_true",
                     help="c3: disabled (see --c3-resident)")
+    ap.add_argument("--c3-key-offset", type=int, default=0,
+                    help="c3 with --c3-resident: add this (rounded down to a multiple of the set count) to "
+                         "every key, e.g. 2**40 for keys wider than 32 bits")
     ap.add_argument("--c3-resident", action="store_true",
                     help="c3: every backing row resident in the cache (loaded as a cache state) before the "
                          "lookups: the hit path alone; no inserts or updates are timed")

@@ -261,3 +261,29 @@ def test_short_bag_kernel_matches_general_kernel_and_oracle(dtype, dim, pooling)
     mapped = np.where(keys < rows, keys, rows)
     ref = oracle_pool(padded, mapped, dtype, dim, O.CSR, pooling, off, bags, 0, w, O.F32, dtype)
     assert np.array_equal(got[0].view(bits), ref.view(bits))
+
+
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_WMEAN])
+def test_short_bags_with_offsets_out_of_order(pooling):
+    """CSR offsets that are not ascending (bags out of order, overlapping, and
+    ends before starts, which make empty bags): the short-bag kernel stages
+    each bag's keys on its own then, and still adds them in key order, bit for
+    bit with the oracle; workgroups with ascending offsets beside them take the
+    shared staging."""
+    rng = np.random.default_rng(77 + pooling)
+    rows, dim, bags = 5000, 128, 300
+    tb = float_table(rng, rows, dim, O.F16, dyadic_values=False)
+    n = 4000
+    keys = rng.integers(0, rows, size=n).astype(np.int64)
+    keys[rng.uniform(size=n) < 0.03] = rows + 9
+    off = np.sort(rng.integers(0, n + 1, size=bags + 1)).astype(np.int64)
+    shuffled = rng.permutation(np.arange(40, 120))  # some workgroups out of order
+    off[40:120] = off[shuffled]
+    off[0], off[-1] = 0, n
+    weighted = pooling == _lib.POOL_WMEAN
+    w = rng.uniform(0, 1, size=n).astype(np.float32) if weighted else None
+    got = run_pool(tb, O.F16, keys, pooling, _lib.SPARSE_CSR, off, bags, 0, w, O.F32, O.F16, 0, 0)
+    padded = np.concatenate([tb, np.zeros((1, tb.shape[1]), np.uint8)])
+    mapped = np.where(keys < rows, keys, rows)
+    ref = oracle_pool(padded, mapped, O.F16, dim, O.CSR, pooling, off, bags, 0, w, O.F32, O.F16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
