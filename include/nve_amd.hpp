@@ -19,9 +19,10 @@
  * same name and throws nve::Exception (the C status and the library's
  * message) when it fails.  Differences from the reference's classes:
  *   - streams are hipStream_t;
- *   - table methods take plain pointers where the reference takes
- *     buffer_ptr<T> (BufferWrapper): host or device memory is accepted and
- *     staged by the library, as BufferWrapper does;
+ *   - table methods take either buffer_ptr<T> (BufferWrapper, as the
+ *     reference's do) or plain pointers; host or device memory is accepted
+ *     either way and staged by the library; BufferWrapper's memory types are
+ *     hipMemoryType and its staging copies belong to the wrapper;
  *   - custom allocators are not supported (pass nullptr / {});
  *   - DataType_t's numeric values are the C ABI's (the names are the
  *     reference's). */
@@ -143,7 +144,106 @@ class ExecutionContext {
 };
 using context_ptr_t = std::shared_ptr<ExecutionContext>;
 
+// A named view of a caller's buffer (the reference's BufferWrapper<T>,
+// include/buffer_wrapper.hpp:34-123): what the reference's table methods take
+// for keys, values, hit masks and sizes.  The table methods below hand the
+// caller's own pointer to the library, which reads host, pinned or device
+// memory itself.  access_buffer gives a caller the buffer in another memory
+// type as the reference's does (allocated on first access, contents copied
+// when asked, a const buffer copied only once); those copies belong to the
+// wrapper and are freed with it (the reference's belong to the context).
+template <typename T>
+class BufferWrapper {
+ public:
+  BufferWrapper(context_ptr_t& ctx, const std::string name, T* buffer, const size_t size_in_bytes)
+      : ctx_(ctx), name_(std::move(name)), size_(size_in_bytes) {
+    if (!ctx_) throw Exception(NVE_ERROR_INVALID_ARGUMENT, "Invalid context");
+    if (!buffer) throw Exception(NVE_ERROR_INVALID_ARGUMENT, "Invalid buffer");
+    last_access_ = type_of(buffer);
+    slots_.push_back({last_access_, buffer, false});
+  }
+  BufferWrapper(const BufferWrapper&) = delete;
+  BufferWrapper& operator=(const BufferWrapper&) = delete;
+  ~BufferWrapper() {
+    for (auto& s : slots_) {
+      if (!s.owned) continue;
+      void* p = const_cast<void*>(static_cast<const void*>(s.ptr));
+      if (s.type == hipMemoryTypeHost)
+        (void)hipHostFree(p);
+      else
+        (void)hipFree(p);
+    }
+  }
+
+  T* access_buffer(hipMemoryType mem_type, bool copy_content, hipStream_t stream) {
+    if (mem_type == hipMemoryTypeUnregistered) mem_type = hipMemoryTypeHost;
+    if (mem_type != hipMemoryTypeHost && mem_type != hipMemoryTypeDevice && !get_buffer(mem_type))
+      throw Exception(NVE_ERROR_INVALID_ARGUMENT, "BufferWrapper '" + name_ + "': cannot allocate this memory type");
+    bool fresh = false;
+    if (!get_buffer(mem_type)) {
+      if (std::is_const<T>::value && !copy_content)
+        throw Exception(NVE_ERROR_INVALID_ARGUMENT,
+                        "BufferWrapper '" + name_ + "': a const buffer must be accessed with copy_content");
+      void* p = nullptr;
+      hipError_t e = mem_type == hipMemoryTypeHost ? hipHostMalloc(&p, size_ ? size_ : 1)
+                                                   : hipMalloc(&p, size_ ? size_ : 1);
+      if (e != hipSuccess) throw Exception(NVE_ERROR_OUT_OF_MEMORY, "BufferWrapper '" + name_ + "': allocation failed");
+      slots_.push_back({mem_type, static_cast<T*>(p), true});
+      fresh = true;
+    }
+    T* dst = get_buffer(mem_type);
+    if (copy_content && (!std::is_const<T>::value || fresh)) {
+      const void* src = static_cast<const void*>(get_buffer(last_access_));
+      void* d = const_cast<void*>(static_cast<const void*>(dst));
+      if (src != d && size_) {
+        if (hipMemcpyAsync(d, src, size_, hipMemcpyDefault, stream) != hipSuccess ||
+            (mem_type != hipMemoryTypeDevice && hipStreamSynchronize(stream) != hipSuccess))
+          throw Exception(NVE_ERROR_CUDA, "BufferWrapper '" + name_ + "': copy failed");
+      }
+    }
+    last_access_ = mem_type;
+    return dst;
+  }
+  hipMemoryType get_last_access() const { return last_access_; }
+  // the buffer of that memory type if the wrapper has one, else nullptr
+  T* get_buffer(hipMemoryType mem_type) const {
+    for (const auto& s : slots_)
+      if (s.type == mem_type) return s.ptr;
+    return nullptr;
+  }
+  // the caller's own buffer, which the table methods pass on
+  T* data() const { return slots_.front().ptr; }
+  size_t size() const { return size_; }
+  const std::string& name() const { return name_; }
+
+ private:
+  struct Slot {
+    hipMemoryType type;
+    T* ptr;
+    bool owned;
+  };
+  static hipMemoryType type_of(const void* p) {
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+      (void)hipGetLastError();
+      return hipMemoryTypeUnregistered;
+    }
+    return a.type;
+  }
+  context_ptr_t ctx_;
+  std::string name_;
+  size_t size_;
+  hipMemoryType last_access_ = hipMemoryTypeUnregistered;
+  std::vector<Slot> slots_;
+};
+template <typename T>
+using buffer_ptr = std::shared_ptr<BufferWrapper<T>>;
+
 namespace detail {
+template <typename T>
+T* ptr_of(const buffer_ptr<T>& b) {
+  return b ? b->data() : nullptr;
+}
 inline nve_thread_pool_t pool_of(const thread_pool_ptr_t& p) { return p ? p->handle() : nullptr; }
 inline void no_allocator(const allocator_ptr_t& a) {
   if (a) throw Exception(NVE_ERROR_INVALID_ARGUMENT, "Custom allocators are not supported by this build");
@@ -226,6 +326,31 @@ class Table {
   }
   void erase(context_ptr_t& ctx, int64_t num_keys, const void* keys) {
     detail::check(nve_table_erase(h_, ctx->handle(), num_keys, keys));
+  }
+
+  // the reference's signatures (include/table.hpp:104-180)
+  template <typename T>
+  using buffer_ptr = nve::buffer_ptr<T>;
+  void find(context_ptr_t& ctx, int64_t n, buffer_ptr<const void> keys, buffer_ptr<bitmask64_t> hit_mask,
+            int64_t value_stride, buffer_ptr<void> values, buffer_ptr<int64_t> value_sizes) const {
+    find(ctx, n, detail::ptr_of(keys), detail::ptr_of(hit_mask), value_stride, detail::ptr_of(values),
+         detail::ptr_of(value_sizes));
+  }
+  void insert(context_ptr_t& ctx, int64_t n, buffer_ptr<const void> keys, int64_t value_stride,
+              int64_t value_size, buffer_ptr<const void> values) {
+    insert(ctx, n, detail::ptr_of(keys), value_stride, value_size, detail::ptr_of(values));
+  }
+  void update(context_ptr_t& ctx, int64_t n, buffer_ptr<const void> keys, int64_t value_stride,
+              int64_t value_size, buffer_ptr<const void> values) {
+    update(ctx, n, detail::ptr_of(keys), value_stride, value_size, detail::ptr_of(values));
+  }
+  void update_accumulate(context_ptr_t& ctx, int64_t n, buffer_ptr<const void> keys, int64_t update_stride,
+                         int64_t update_size, buffer_ptr<const void> updates, DataType_t update_dtype) {
+    update_accumulate(ctx, n, detail::ptr_of(keys), update_stride, update_size, detail::ptr_of(updates),
+                      update_dtype);
+  }
+  void erase(context_ptr_t& ctx, int64_t n, buffer_ptr<const void> keys) {
+    erase(ctx, n, detail::ptr_of(keys));
   }
   void clear(context_ptr_t& ctx) { detail::check(nve_table_clear(h_, ctx->handle())); }
   context_ptr_t create_execution_context(hipStream_t lookup_stream, hipStream_t modify_stream,

@@ -6,6 +6,11 @@
 //   cpp_api_check host   LinearHostTable + HostEmbeddingLayer (no GPU needed)
 //   cpp_api_check gpu    GPUEmbeddingLayer, GpuTable + LinearUVMEmbeddingLayer
 //
+// Both modes also call the tables through the reference's buffer_ptr<T>
+// (BufferWrapper) signatures: find with a hit mask, update_accumulate on the
+// host table; find, update and erase on the GPU table with keys staged on the
+// device by BufferWrapper::access_buffer.
+//
 // Tables hold multiples of 1/64 in [-1, 1), so every sum of up to 256 of them
 // is exact in fp32 and the pooled results are compared bit for bit with a
 // plain loop.  Prints "<mode> ok" and exits 0, or names the first mismatch
@@ -13,6 +18,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <random>
 #include <vector>
@@ -94,6 +100,40 @@ int run_host() {
   std::vector<float> found(want_g.size());
   host_table->find(tctx, (int64_t)keys.size(), keys.data(), nullptr, dim * 4, found.data(), nullptr);
   if (!same(found, want_g)) return fail("host table find");
+  {
+    // the reference's buffer_ptr signatures (table.hpp:104-180)
+    const int64_t n = (int64_t)keys.size();
+    auto kb = std::make_shared<nve::BufferWrapper<const void>>(tctx, "keys", keys.data(), keys.size() * 8);
+    std::vector<float> found2(want_g.size());
+    std::vector<nve::bitmask64_t> mask((size_t)((n + 63) / 64), 0);
+    auto vb = std::make_shared<nve::BufferWrapper<void>>(tctx, "values", found2.data(), found2.size() * 4);
+    auto mb = std::make_shared<nve::BufferWrapper<nve::bitmask64_t>>(tctx, "hit_mask", mask.data(), mask.size() * 8);
+    host_table->find(tctx, n, kb, mb, dim * 4, vb, nullptr);
+    tctx->wait();
+    if (!same(found2, want_g)) return fail("host table find through buffer_ptr");
+    for (int64_t i = 0; i < n; ++i)
+      if (!((mask[(size_t)(i / 64)] >> (i % 64)) & 1)) return fail("host table hit mask through buffer_ptr");
+    // +1 on the first key's row, then read it back
+    std::vector<float> ones((size_t)dim, 1.0f), row((size_t)dim);
+    auto k0 = std::make_shared<nve::BufferWrapper<const void>>(tctx, "k0", keys.data(), 8);
+    auto ub = std::make_shared<nve::BufferWrapper<const void>>(tctx, "updates", ones.data(), ones.size() * 4);
+    auto rb = std::make_shared<nve::BufferWrapper<void>>(tctx, "row", row.data(), row.size() * 4);
+    host_table->update_accumulate(tctx, 1, k0, dim * 4, dim * 4, ub, nve::DataType_t::Float32);
+    host_table->find(tctx, 1, k0, nullptr, dim * 4, rb, nullptr);
+    tctx->wait();
+    for (int64_t e = 0; e < dim; ++e)
+      if (row[(size_t)e] != want_g[(size_t)e] + 1.0f) return fail("host update_accumulate through buffer_ptr");
+    if (kb->get_buffer(hipMemoryTypeDevice) != nullptr || kb->data() != keys.data())
+      return fail("BufferWrapper made a copy nobody asked for");
+    // updates of another type than the table's are refused (as the
+    // reference's LinearHostTable accumulates into Float32 rows only)
+    try {
+      host_table->update_accumulate(tctx, 1, k0, dim * 4, dim * 4, ub, nve::DataType_t::Float16);
+      return fail("Float16 updates into a Float32 host table accepted");
+    } catch (const nve::Exception& e) {
+      if (e.status() != NVE_ERROR_RUNTIME) return fail("wrong status for a mixed-type accumulate");
+    }
+  }
   // errors surface as nve::Exception with the C status
   try {
     layer.lookup(ctx, 4, nullptr, got_g.data(), dim * 4, nullptr, nullptr, nullptr);
@@ -102,6 +142,61 @@ int run_host() {
     if (e.status() != NVE_ERROR_INVALID_ARGUMENT) return fail("wrong status for null keys");
   }
   std::printf("host ok\n");
+  return 0;
+}
+
+// find / update / erase of a GPU table through the reference's buffer_ptr
+// signatures, the keys staged on the device by BufferWrapper::access_buffer;
+// keys[0..511] are resident
+int table_through_buffer_ptr(std::shared_ptr<nve::GpuTable<int64_t>>& gt, nve::context_ptr_t& tctx, hipStream_t s,
+                             const std::vector<int64_t>& keys, const std::vector<float>& want_g, int64_t dim) {
+  const int64_t n = 512, words = n / 64;
+  auto host_keys = std::make_shared<nve::BufferWrapper<const void>>(tctx, "keys", keys.data(), n * 8);
+  const void* dk = host_keys->access_buffer(hipMemoryTypeDevice, true, s);
+  if (dk == nullptr || dk == keys.data() || host_keys->get_last_access() != hipMemoryTypeDevice)
+    return fail("access_buffer did not stage the keys on the device");
+  auto kb = std::make_shared<nve::BufferWrapper<const void>>(tctx, "dkeys", dk, n * 8);
+  std::vector<float> vals((size_t)(n * dim));
+  std::vector<nve::bitmask64_t> mask((size_t)words);
+  auto vb = std::make_shared<nve::BufferWrapper<void>>(tctx, "values", vals.data(), vals.size() * 4);
+  auto mb = std::make_shared<nve::BufferWrapper<nve::bitmask64_t>>(tctx, "hit_mask", mask.data(), mask.size() * 8);
+  auto find = [&]() {
+    std::fill(mask.begin(), mask.end(), 0);
+    gt->find(tctx, n, kb, mb, dim * 4, vb, nullptr);
+    tctx->wait();
+    return hipStreamSynchronize(s) == hipSuccess;
+  };
+  auto hit = [&](int64_t i) { return (mask[(size_t)(i / 64)] >> (i % 64)) & 1; };
+  auto row_is = [&](int64_t i, const float* want) {
+    return std::memcmp(&vals[(size_t)(i * dim)], want, (size_t)dim * 4) == 0;
+  };
+  if (!find()) return fail("find through buffer_ptr");
+  for (int64_t i = 0; i < n; ++i)
+    if (!hit(i) || !row_is(i, &want_g[(size_t)(i * dim)])) return fail("GPU table find through buffer_ptr");
+  // new rows for keys[16..31], then keys[0..7] erased; the new rows must
+  // come back and the erased keys miss (as do later copies of them)
+  std::vector<float> upd((size_t)(16 * dim));
+  for (size_t j = 0; j < upd.size(); ++j) upd[j] = -(float)(j % 97) / 8.0f;
+  auto uk = std::make_shared<nve::BufferWrapper<const void>>(tctx, "ukeys", keys.data() + 16, 16 * 8);
+  auto ub = std::make_shared<nve::BufferWrapper<const void>>(tctx, "updates", upd.data(), upd.size() * 4);
+  auto ek = std::make_shared<nve::BufferWrapper<const void>>(tctx, "ekeys", keys.data(), 8 * 8);
+  gt->update(tctx, 16, uk, dim * 4, dim * 4, ub);
+  gt->erase(tctx, 8, ek);
+  if (!find()) return fail("find after update / erase");
+  for (int64_t i = 0; i < n; ++i) {
+    bool erased = false;
+    for (int64_t j = 0; j < 8; ++j) erased = erased || keys[(size_t)i] == keys[(size_t)j];
+    int64_t upd_row = -1;  // the last update of this key wins
+    for (int64_t j = 0; j < 16; ++j)
+      if (keys[(size_t)i] == keys[(size_t)(16 + j)]) upd_row = j;
+    if (erased) {
+      if (hit(i)) return fail("an erased key still hits");
+    } else if (!hit(i)) {
+      return fail("a resident key missed after update / erase");
+    } else if (upd_row >= 0 ? !row_is(i, &upd[(size_t)(upd_row * dim)]) : !row_is(i, &want_g[(size_t)(i * dim)])) {
+      return fail("GPU table update through buffer_ptr");
+    }
+  }
   return 0;
 }
 
@@ -166,6 +261,7 @@ int run_gpu() {
       ctx->wait();
       HIP_OK(hipStreamSynchronize(s));
       if (!same(got_g, want_g)) rc = fail("LinearUVM layer gather");
+      if (!rc) rc = table_through_buffer_ptr(gt, tctx, s, keys, want_g, dim);
     }
     gt.reset();
     HIP_OK(hipHostFree(backing));
