@@ -8,8 +8,8 @@
 //
 // Both modes also call the tables through the reference's buffer_ptr<T>
 // (BufferWrapper) signatures: find with a hit mask, update_accumulate on the
-// host table; find, update and erase on the GPU table with keys staged on the
-// device by BufferWrapper::access_buffer.
+// host table; insert, find, update and erase on a cache-only GPU table with
+// keys staged on the device by BufferWrapper::access_buffer.
 //
 // Tables hold multiples of 1/64 in [-1, 1), so every sum of up to 256 of them
 // is exact in fp32 and the pooled results are compared bit for bit with a
@@ -17,8 +17,8 @@
 // and exits 1.
 #include <hip/hip_runtime_api.h>
 
-#include <cstdio>
 #include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <random>
 #include <vector>
@@ -145,23 +145,32 @@ int run_host() {
   return 0;
 }
 
-// find / update / erase of a GPU table through the reference's buffer_ptr
-// signatures, the keys staged on the device by BufferWrapper::access_buffer;
-// keys[0..511] are resident
-int table_through_buffer_ptr(std::shared_ptr<nve::GpuTable<int64_t>>& gt, nve::context_ptr_t& tctx, hipStream_t s,
-                             const std::vector<int64_t>& keys, const std::vector<float>& want_g, int64_t dim) {
+// insert / find / update / erase of a cache-only GPU table (so that the hit
+// mask means residency) through the reference's buffer_ptr signatures, the
+// keys staged on the device by BufferWrapper::access_buffer
+int table_through_buffer_ptr(hipStream_t s, const std::vector<int64_t>& keys, const std::vector<float>& want_g,
+                             int64_t dim) {
   const int64_t n = 512, words = n / 64;
+  nve::GPUTableConfig tc;
+  tc.cache_size = 2 << 20;  // 1024 sets of 8 ways: 512 keys all fit
+  tc.row_size_in_bytes = dim * 4;
+  tc.value_dtype = nve::DataType_t::Float32;
+  auto gt = std::make_shared<nve::GpuTable<int64_t>>(tc);
+  auto tctx = gt->create_execution_context(s, s);
   auto host_keys = std::make_shared<nve::BufferWrapper<const void>>(tctx, "keys", keys.data(), n * 8);
   const void* dk = host_keys->access_buffer(hipMemoryTypeDevice, true, s);
   if (dk == nullptr || dk == keys.data() || host_keys->get_last_access() != hipMemoryTypeDevice)
     return fail("access_buffer did not stage the keys on the device");
   auto kb = std::make_shared<nve::BufferWrapper<const void>>(tctx, "dkeys", dk, n * 8);
+  auto rows = std::make_shared<nve::BufferWrapper<const void>>(tctx, "rows", want_g.data(), (size_t)(n * dim) * 4);
+  gt->insert(tctx, n, kb, dim * 4, dim * 4, rows);
   std::vector<float> vals((size_t)(n * dim));
   std::vector<nve::bitmask64_t> mask((size_t)words);
   auto vb = std::make_shared<nve::BufferWrapper<void>>(tctx, "values", vals.data(), vals.size() * 4);
   auto mb = std::make_shared<nve::BufferWrapper<nve::bitmask64_t>>(tctx, "hit_mask", mask.data(), mask.size() * 8);
   auto find = [&]() {
     std::fill(mask.begin(), mask.end(), 0);
+    std::fill(vals.begin(), vals.end(), 0.0f);
     gt->find(tctx, n, kb, mb, dim * 4, vb, nullptr);
     tctx->wait();
     return hipStreamSynchronize(s) == hipSuccess;
@@ -172,9 +181,9 @@ int table_through_buffer_ptr(std::shared_ptr<nve::GpuTable<int64_t>>& gt, nve::c
   };
   if (!find()) return fail("find through buffer_ptr");
   for (int64_t i = 0; i < n; ++i)
-    if (!hit(i) || !row_is(i, &want_g[(size_t)(i * dim)])) return fail("GPU table find through buffer_ptr");
-  // new rows for keys[16..31], then keys[0..7] erased; the new rows must
-  // come back and the erased keys miss (as do later copies of them)
+    if (!hit(i) || !row_is(i, &want_g[(size_t)(i * dim)])) return fail("GPU table insert + find through buffer_ptr");
+  // new rows for keys[16..31], then keys[0..7] erased: the erased keys (and
+  // later copies of them) miss, the updated ones return a new row
   std::vector<float> upd((size_t)(16 * dim));
   for (size_t j = 0; j < upd.size(); ++j) upd[j] = -(float)(j % 97) / 8.0f;
   auto uk = std::make_shared<nve::BufferWrapper<const void>>(tctx, "ukeys", keys.data() + 16, 16 * 8);
@@ -184,16 +193,18 @@ int table_through_buffer_ptr(std::shared_ptr<nve::GpuTable<int64_t>>& gt, nve::c
   gt->erase(tctx, 8, ek);
   if (!find()) return fail("find after update / erase");
   for (int64_t i = 0; i < n; ++i) {
-    bool erased = false;
+    bool erased = false, updated = false, match = false;
     for (int64_t j = 0; j < 8; ++j) erased = erased || keys[(size_t)i] == keys[(size_t)j];
-    int64_t upd_row = -1;  // the last update of this key wins
-    for (int64_t j = 0; j < 16; ++j)
-      if (keys[(size_t)i] == keys[(size_t)(16 + j)]) upd_row = j;
+    for (int64_t j = 0; j < 16; ++j)  // a key given twice may keep either row
+      if (keys[(size_t)i] == keys[(size_t)(16 + j)]) {
+        updated = true;
+        match = match || row_is(i, &upd[(size_t)(j * dim)]);
+      }
     if (erased) {
       if (hit(i)) return fail("an erased key still hits");
     } else if (!hit(i)) {
       return fail("a resident key missed after update / erase");
-    } else if (upd_row >= 0 ? !row_is(i, &upd[(size_t)(upd_row * dim)]) : !row_is(i, &want_g[(size_t)(i * dim)])) {
+    } else if (updated ? !match : !row_is(i, &want_g[(size_t)(i * dim)])) {
       return fail("GPU table update through buffer_ptr");
     }
   }
@@ -261,11 +272,11 @@ int run_gpu() {
       ctx->wait();
       HIP_OK(hipStreamSynchronize(s));
       if (!same(got_g, want_g)) rc = fail("LinearUVM layer gather");
-      if (!rc) rc = table_through_buffer_ptr(gt, tctx, s, keys, want_g, dim);
     }
     gt.reset();
     HIP_OK(hipHostFree(backing));
   }
+  if (!rc) rc = table_through_buffer_ptr(s, keys, want_g, dim);
   HIP_OK(hipStreamDestroy(s));
   HIP_OK(hipFree(d_table));
   if (!rc) std::printf("gpu ok\n");
