@@ -81,6 +81,21 @@ hipError_t launch_counter_total(unsigned long long* words, int n, unsigned long 
   return hipGetLastError();
 }
 
+// A readback of a few bytes (counts and spans between the launches of an
+// insert or a dedup): one wave stores them into pinned host memory, which
+// costs less than a copy-engine transfer queued behind the kernels.
+__global__ __launch_bounds__(64) void small_read_kernel(const uint8_t* src, uint8_t* dst, int bytes) {
+  const int i = (int)threadIdx.x;
+  if (i < bytes) dst[i] = src[i];
+}
+
+hipError_t launch_small_read(void* host_dst, const void* dev_src, int bytes, hipStream_t stream) {
+  if (bytes <= 0 || bytes > 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(small_read_kernel, dim3(1), dim3(64), 0, stream, static_cast<const uint8_t*>(dev_src),
+                     static_cast<uint8_t*>(host_dst), bytes);
+  return hipGetLastError();
+}
+
 hipError_t launch_cache_erase(void* tags, const void* keys, int64_t n, int key_bytes,
                               uint64_t num_sets, int64_t sentinel, hipStream_t stream) {
   if (n <= 0) return hipSuccess;

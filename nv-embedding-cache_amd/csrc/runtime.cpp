@@ -15,7 +15,7 @@ void read_small(void* host, const void* dev, size_t bytes, hipStream_t stream) {
   // one pinned slot per thread, kept for the thread's life
   thread_local void* slot = nullptr;
   if (slot == nullptr) NVE_HIP(hipHostMalloc(&slot, 64, hipHostMallocDefault));
-  NVE_HIP(hipMemcpyAsync(slot, dev, bytes, hipMemcpyDeviceToHost, stream));
+  NVE_HIP(launch_small_read(slot, dev, (int)bytes, stream));
   NVE_HIP(hipStreamSynchronize(stream));
   std::memcpy(host, slot, bytes);
 }
