@@ -15,6 +15,7 @@
 #include <cstring>
 
 #include "kernels/cache_launch.hpp"
+#include "kernels/modify_launch.hpp"
 #include "layers.hpp"
 #include "trace.hpp"
 
@@ -64,6 +65,8 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
     NVE_HIP(hipMalloc((void**)&set_ts_, (size_t)num_sets_ * sizeof(int64_t)));
     NVE_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(counters_), (int64_t)ways, 0, nullptr));
     NVE_HIP(launch_fill_u64(reinterpret_cast<uint64_t*>(set_ts_), (int64_t)num_sets_, 0, nullptr));
+    NVE_HIP(hipMalloc((void**)&set_word_, (size_t)num_sets_ * sizeof(uint64_t)));
+    NVE_HIP(launch_fill_u64(set_word_, (int64_t)num_sets_, kSetClean, nullptr));
     build_decay_table();
   } else {
     h_tags_.resize((size_t)ways * key_bytes);
@@ -84,6 +87,7 @@ GpuTable::~GpuTable() {
   (void)hipFree(tags_);
   (void)hipFree(counters_);
   (void)hipFree(set_ts_);
+  (void)hipFree(set_word_);
   (void)hipFree(decay_table_);
 }
 

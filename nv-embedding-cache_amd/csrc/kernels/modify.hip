@@ -24,6 +24,8 @@
 // comes from a table of (float)pow((double)rate, (double)delta) built on the
 // host; the reference computes it with CUDA's __powf, whose bits are not
 // published.
+#include <algorithm>
+
 #include "device_common.cuh"
 #include "modify_launch.hpp"
 #include "sort_launch.hpp"
@@ -175,14 +177,17 @@ __device__ __forceinline__ void merge_block8(float& p1, uint32_t& pos1, float p2
   }
 }
 
-template <typename K, typename UK>
-__global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
-  const int x = threadIdx.x & 7;
-  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
-  if (r >= a.num_rsets) return;  // whole 8-lane groups leave together
-  const uint32_t set = a.rset[r];
-  const uint32_t base = a.roff[r];
-  const uint32_t cnt = a.roff[r + 1] - base;
+// The replacement of one set by its 8-lane group (this lane: x).  The set's
+// cnt candidates come in histogram order: cand(t, &key, &prio) fetches
+// candidate t, id(t) names it; the id travels through the networks (as a
+// float through MergeBlock, as in the reference) and key_of(id) gives the
+// winner's key back.  record(x, write, slot, tag, id) stores lane x's outcome
+// (x < min(cnt, 8)); no_record(j) marks the set's record position j >= 8 empty.
+template <typename K, typename UK, typename Cand, typename Id, typename KeyOf, typename Record,
+          typename NoRecord>
+__device__ __forceinline__ void replace_set(const ReplaceLaunch& a, uint32_t set, uint32_t cnt, int x,
+                                            Cand cand, Id id, KeyOf key_of, Record record,
+                                            NoRecord no_record) {
   const K* tags = static_cast<const K*>(a.tags) + (uint64_t)set * 8;
   float* ctr = a.counters + (uint64_t)set * 8;
   const UK ns = (UK)a.num_sets;
@@ -206,9 +211,11 @@ __global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
     uint32_t hit_ways = 0;  // every way holding this candidate's key
     float prio = 0.0f;
     if (done + x < cnt) {
-      const uint32_t loc = a.order[base + done + x];
-      const K key = (K)a.hkeys[loc];
-      prio = a.hprio[loc];
+      const uint32_t t = done + (uint32_t)x;
+      const uint32_t loc = id(t);
+      int64_t k64;
+      cand(t, &k64, &prio);
+      const K key = (K)k64;
       for (int w = 0; w < 8; ++w) {
         const K tw = tags[w];
         if ((K)((UK)tw * ns + (UK)set) == key) hit_ways |= 1u << w;
@@ -241,22 +248,11 @@ __global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
   const float rc = g8f(cv, 7 - x);
   const uint32_t num_repl = cnt < 8 ? cnt : 8;
   const bool write = ((uint32_t)x < num_repl) && (best > rc);
-  // records at the set's own positions of the order: lane x's at base + x
-  // (x < num_repl <= cnt), every other position of the set marked empty (a
-  // counter of records bumped by each replacing wave serialized thousands of
-  // same-address atomics at the memory side: 70 us per 262,144-key insert)
   if ((uint32_t)x < cnt) {
-    const uint32_t pos = base + x;
-    if (write) {
-      const int64_t key = a.hkeys[best_pos];
-      a.rec_slot[pos] = (uint64_t)set * 8 + rd;
-      a.rec_tag[pos] = (int64_t)(K)((UK)(K)key / ns);  // embed_cache_construct_tag
-      a.rec_src[pos] = a.hsrc[best_pos];
-    } else {
-      a.rec_slot[pos] = kNoRecord;
-    }
+    const int64_t key = write ? key_of(best_pos) : 0;
+    record(x, write, (uint64_t)set * 8 + rd, (int64_t)(K)((UK)(K)key / ns), best_pos);  // embed_cache_construct_tag
   }
-  for (uint32_t j = 8 + x; j < cnt; j += 8) a.rec_slot[base + j] = kNoRecord;
+  for (uint32_t j = 8 + x; j < cnt; j += 8) no_record(j);
   // the replaced way's counter becomes the winner's priority
   for (int sl = 0; sl < 8; ++sl) {
     const int wr = __shfl((int)write, sl, 8);
@@ -266,6 +262,313 @@ __global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
   }
   ctr[x] = c;
   if (x == 0) a.set_ts[set] = a.global_ts;
+}
+
+// Sorted histogram: set r's candidates are a.order[roff[r] .. roff[r+1]).
+// Records at the set's own positions of the order: lane x's at base + x
+// (x < num_repl <= cnt), every other position of the set marked empty (a
+// counter of records bumped by each replacing wave serialized thousands of
+// same-address atomics at the memory side: 70 us per 262,144-key insert).
+template <typename K, typename UK>
+__global__ __launch_bounds__(256) void set_replace_kernel(ReplaceLaunch a) {
+  const int x = threadIdx.x & 7;
+  const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+  if (r >= a.num_rsets) return;  // whole 8-lane groups leave together
+  const uint32_t set = a.rset[r];
+  const uint32_t base = a.roff[r];
+  const uint32_t cnt = a.roff[r + 1] - base;
+  // a candidate's id is its histogram index
+  auto id = [&](uint32_t t) { return a.order[base + t]; };
+  auto cand = [&](uint32_t t, int64_t* key, float* prio) {
+    const uint32_t loc = a.order[base + t];
+    *key = a.hkeys[loc];
+    *prio = a.hprio[loc];
+  };
+  auto key_of = [&](uint32_t loc) { return a.hkeys[loc]; };
+  auto record = [&](int lx, bool write, uint64_t slot, int64_t tag, uint32_t loc) {
+    const uint32_t pos = base + (uint32_t)lx;
+    if (write) {
+      a.rec_slot[pos] = slot;
+      a.rec_tag[pos] = tag;
+      a.rec_src[pos] = a.hsrc[loc];
+    } else {
+      a.rec_slot[pos] = kNoRecord;
+    }
+  };
+  auto no_record = [&](uint32_t j) { a.rec_slot[base + j] = kNoRecord; };
+  replace_set<K, UK>(a, set, cnt, x, cand, id, key_of, record, no_record);
+}
+
+// ---------------------------------------------------------------------------
+// hashed histogram (large caches: num_sets >= batch size)
+//
+// The sorted histogram above takes ten radix passes and two readbacks for a
+// 262,144-key batch.  Here the batch's unique keys, their counts and first
+// positions come from a hash table (a workgroup dedups its 1,024 keys in LDS
+// first, so a key is claimed once per workgroup); each unique key is chained
+// into its set through a per-set word (candidate count << 32 | chain head),
+// which the table keeps clean between inserts; and the replacement of a set
+// sorts its few candidates into the histogram's order -- count descending,
+// then key ascending in the key's signed order, which is the order the stable
+// sorts give -- before running the same per-set replacement.  Positions
+// passing through the networks are then the candidates' places in their set,
+// so they are exact.  A set with more than kHashSetMax candidates sets the
+// overflow word; the replacement then only cleans up and the host falls back
+// to the sorted histogram (nothing of the cache has changed).
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr uint64_t kHashEmpty = ~0ull;
+constexpr int kHashLocalBits = 11;  // 2,048 LDS slots for a workgroup's 1,024 keys
+
+// Fibonacci hash to `bits` bits
+__device__ __forceinline__ uint32_t hins_hash(uint64_t k, int bits) {
+  return (uint32_t)((k * 0x9E3779B97F4A7C15ull) >> (64 - bits));
+}
+
+// Claims k's slot of a linear-probing table of 2^bits 64-bit slots (k is never
+// kHashEmpty; the caller guarantees a free slot).  *won: this call put k there.
+__device__ __forceinline__ uint32_t hins_claim(uint64_t* tab, uint64_t k, int bits, bool* won) {
+  const uint32_t mask = (1u << bits) - 1u;
+  uint32_t h = hins_hash(k, bits);
+  for (;;) {
+    const uint64_t cur = (uint64_t)atomicCAS(reinterpret_cast<unsigned long long*>(tab + h),
+                                             (unsigned long long)kHashEmpty, (unsigned long long)k);
+    if (cur == kHashEmpty || cur == k) {
+      *won = cur == kHashEmpty;
+      return h;
+    }
+    h = (h + 1) & mask;
+  }
+}
+
+// Appends v to list[base + i] for every thread with app set, one global
+// atomic per workgroup (all threads of the workgroup call it).
+__device__ __forceinline__ void wg_append(bool app, uint32_t v, uint32_t* counter, uint32_t* list,
+                                          uint32_t* s_wave, uint32_t* s_base) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwaves = (int)(blockDim.x + 63) >> 6;
+  const uint64_t bal = __ballot(app);
+  const uint32_t below = (uint32_t)__popcll(bal & (lane == 0 ? 0ull : (~0ull >> (64 - lane))));
+  if (lane == 0) s_wave[wave] = (uint32_t)__popcll(bal);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < nwaves; ++w) {
+      const uint32_t c = s_wave[w];
+      s_wave[w] = run;
+      run += c;
+    }
+    *s_base = run ? atomicAdd(counter, run) : 0u;
+  }
+  __syncthreads();
+  if (app) list[*s_base + s_wave[wave] + below] = v;
+}
+
+}  // namespace
+
+// The hash table emptied, the counts zeroed and every record position marked
+// empty (2^bits + 1 > n threads).
+__global__ __launch_bounds__(256) void hins_clear_kernel(HashInsertLaunch a, uint64_t* rec_slot) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t slots = (1ll << a.bits) + 1;
+  if (i < slots) {
+    a.tkey[i] = kHashEmpty;
+    a.tcount[i] = 0u;
+    a.tfirst[i] = 0xffffffffu;
+  }
+  if (i < a.n) rec_slot[i] = kNoRecord;
+  if (i < 4) a.counts[i] = 0u;
+}
+
+// Counts and first positions of the batch's unique keys; the slots of the
+// unique keys listed in ulist[0 .. counts[0]).  Keys are held as 64-bit words
+// (32-bit keys zero-extended); the word kHashEmpty (a 64-bit key of -1) uses
+// the extra slot 2^bits.
+__global__ __launch_bounds__(1024) void hins_count_kernel(HashInsertLaunch a) {
+  __shared__ uint64_t lkey[1 << kHashLocalBits];
+  __shared__ uint32_t lcnt[1 << kHashLocalBits];
+  __shared__ uint32_t lfirst[1 << kHashLocalBits];
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_base;
+  const int tid = threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * 1024 + tid;
+  const uint32_t special = 1u << a.bits;
+  const bool in = i < a.n;
+  uint64_t k = 0;
+  if (in)
+    k = a.key_bytes == 4 ? (uint64_t)(uint32_t) reinterpret_cast<const int32_t*>(a.keys)[i]
+                         : (uint64_t) reinterpret_cast<const int64_t*>(a.keys)[i];
+  for (int j = tid; j < (1 << kHashLocalBits); j += 1024) {
+    lkey[j] = kHashEmpty;
+    lcnt[j] = 0u;
+    lfirst[j] = 0xffffffffu;
+  }
+  __syncthreads();
+  uint32_t ls = 0;
+  bool first = false, won = false;
+  if (in && k != kHashEmpty) {
+    // the workgroup's own table: one entry per distinct key, its count and first position
+    const uint32_t mask = (1u << kHashLocalBits) - 1u;
+    uint32_t h = hins_hash(k, kHashLocalBits);
+    for (;;) {
+      const uint64_t cur = (uint64_t)atomicCAS(reinterpret_cast<unsigned long long*>(lkey + h),
+                                               (unsigned long long)kHashEmpty, (unsigned long long)k);
+      if (cur == kHashEmpty || cur == k) {
+        first = cur == kHashEmpty;
+        break;
+      }
+      h = (h + 1) & mask;
+    }
+    ls = h;
+    atomicAdd(&lcnt[ls], 1u);
+    atomicMin(&lfirst[ls], (uint32_t)i);
+  } else if (in) {  // the key word kHashEmpty: its own slot
+    atomicAdd(&a.tcount[special], 1u);
+    atomicMin(&a.tfirst[special], (uint32_t)i);
+    won = atomicCAS(reinterpret_cast<unsigned long long*>(a.tkey + special), (unsigned long long)kHashEmpty,
+                    0ull) == (unsigned long long)kHashEmpty;
+  }
+  __syncthreads();
+  uint32_t gs = special;
+  if (first) {
+    gs = hins_claim(a.tkey, k, a.bits, &won);
+    atomicAdd(&a.tcount[gs], lcnt[ls]);
+    atomicMin(&a.tfirst[gs], lfirst[ls]);
+  }
+  wg_append(won, gs, &a.counts[0], a.ulist, s_wave, &s_base);
+}
+
+// The signed histogram key of a unique key's slot (the extra slot: key -1).
+__device__ __forceinline__ int64_t hins_key(const HashInsertLaunch& a, uint32_t gs) {
+  if (gs == (1u << a.bits)) return -1;
+  const uint64_t w = a.tkey[gs];
+  return a.key_bytes == 4 ? (int64_t)(int32_t)(uint32_t)w : (int64_t)w;
+}
+
+// Chains each unique key u < counts[0] into its set; the first key of a set
+// lists the set in rsets[0 .. counts[1]); a set past kHashSetMax candidates
+// sets counts[2].
+__global__ __launch_bounds__(256) void hins_chain_kernel(HashInsertLaunch a) {
+  __shared__ uint32_t s_wave[4];
+  __shared__ uint32_t s_base;
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t nu = a.counts[0];
+  bool first_of_set = false;
+  uint32_t set = 0;
+  if (u < nu) {
+    const int64_t key = hins_key(a, a.ulist[u]);
+    set = a.key_bytes == 4 ? (uint32_t)((uint32_t)(int32_t)key % (uint32_t)a.num_sets)
+                           : (uint32_t)((uint64_t)key % a.num_sets);
+    unsigned long long* w = reinterpret_cast<unsigned long long*>(a.set_word + set);
+    unsigned long long old = *w;
+    for (;;) {
+      const unsigned long long nw = ((unsigned long long)((uint32_t)(old >> 32) + 1u) << 32) | (uint32_t)u;
+      const unsigned long long seen = atomicCAS(w, old, nw);
+      if (seen == old) break;
+      old = seen;
+    }
+    a.unext[u] = (uint32_t)old;  // the previous head (0xffffffff: none)
+    const uint32_t before = (uint32_t)(old >> 32);
+    first_of_set = before == 0;
+    if (before + 1 > (uint32_t)kHashSetMax) a.counts[2] = 1u;
+  }
+  wg_append(first_of_set, set, &a.counts[1], a.rsets, s_wave, &s_base);
+}
+
+// One 8-lane group per touched set (grid-stride): the set's candidates from
+// its chain into LDS, sorted into histogram order, then replace_set.  Records
+// go to the candidates' unique indices (rec_* [0, counts[0])).  Every set's
+// word is cleaned.  On overflow nothing is replaced: every record is marked
+// empty and the words are cleaned.
+template <typename K, typename UK>
+__global__ __launch_bounds__(256) void hins_replace_kernel(HashInsertLaunch h, ReplaceLaunch a) {
+  constexpr int kGroups = 256 / 8;
+  __shared__ int64_t s_key[kGroups][kHashSetMax];
+  __shared__ uint32_t s_cnt[kGroups][kHashSetMax];
+  __shared__ uint32_t s_first[kGroups][kHashSetMax];
+  __shared__ uint32_t s_u[kGroups][kHashSetMax];
+  __shared__ uint32_t s_ord[kGroups][kHashSetMax];
+  __shared__ uint32_t s_n[kGroups];
+  const int x = threadIdx.x & 7;
+  const int g = threadIdx.x >> 3;
+  const int64_t group = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;
+  const int64_t groups = ((int64_t)gridDim.x * blockDim.x) >> 3;
+  const uint32_t nu = h.counts[0];
+  const uint32_t nrs = h.counts[1];
+  if (h.counts[2] != 0u) {  // overflow: clean up only (uniform)
+    for (int64_t u = group * 8 + x; u < nu; u += groups * 8) a.rec_slot[u] = kNoRecord;
+    for (int64_t r = group * 8 + x; r < nrs; r += groups * 8) h.set_word[h.rsets[r]] = kSetClean;
+    return;
+  }
+  const float norm = h.norm;
+  for (int64_t r = group; r < nrs; r += groups) {  // uniform over the 8-lane group
+    const uint32_t set = h.rsets[r];
+    const uint64_t word = h.set_word[set];
+    if (x == 0) {
+      // the chain, at most kHashSetMax long (no overflow) and inside [0, nu)
+      const uint32_t want = (uint32_t)(word >> 32);
+      uint32_t u = (uint32_t)word, j = 0;
+      while (j < want && j < (uint32_t)kHashSetMax && u < nu) {
+        s_u[g][j++] = u;
+        u = h.unext[u];
+      }
+      s_n[g] = j;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t cnt = s_n[g];
+    for (uint32_t j = (uint32_t)x; j < cnt; j += 8) {
+      const uint32_t gs = h.ulist[s_u[g][j]];
+      s_key[g][j] = hins_key(h, gs);
+      s_cnt[g][j] = h.tcount[gs];
+      s_first[g][j] = h.tfirst[gs];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // histogram order: count descending, then key ascending (the key's signed order)
+    for (uint32_t j = (uint32_t)x; j < cnt; j += 8) {
+      const uint32_t cj = s_cnt[g][j];
+      const int64_t kj = s_key[g][j];
+      uint32_t rank = 0;
+      for (uint32_t i = 0; i < cnt; ++i) {
+        const uint32_t ci = s_cnt[g][i];
+        rank += (ci > cj || (ci == cj && s_key[g][i] < kj)) ? 1u : 0u;
+      }
+      s_ord[g][rank] = j;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    auto id = [&](uint32_t t) { return t; };
+    auto cand = [&](uint32_t t, int64_t* key, float* prio) {
+      const uint32_t j = s_ord[g][t];
+      *key = s_key[g][j];
+      *prio = (float)(int32_t)s_cnt[g][j] * norm;
+    };
+    auto key_of = [&](uint32_t t) { return s_key[g][s_ord[g][t]]; };
+    auto record = [&](int lx, bool write, uint64_t slot, int64_t tag, uint32_t t) {
+      const uint32_t pos = s_u[g][lx];
+      if (write) {
+        const uint32_t j = s_ord[g][t];
+        const int64_t idx = h.by_key ? s_key[g][j] : (int64_t)s_first[g][j];
+        a.rec_slot[pos] = slot;
+        a.rec_tag[pos] = tag;
+        a.rec_src[pos] = (uint64_t)h.rows_base + (uint64_t)idx * (uint64_t)h.row_stride;
+      } else {
+        a.rec_slot[pos] = kNoRecord;
+      }
+    };
+    auto no_record = [&](uint32_t j) { a.rec_slot[s_u[g][j]] = kNoRecord; };
+    replace_set<K, UK>(a, set, cnt, x, cand, id, key_of, record, no_record);
+    if (x == 0) h.set_word[set] = kSetClean;
+    // the group's LDS is rewritten for its next set
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -293,14 +596,16 @@ template <int VB>
 __global__ __launch_bounds__(256) void copy_rows_kernel(const uint32_t* num, uint32_t max_records,
                                                         const uint64_t* slot, const uint64_t* src,
                                                         uint8_t* data, uint64_t row_bytes) {
-  const int64_t rec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   const uint32_t n = num != nullptr && *num < max_records ? *num : max_records;
-  if (rec >= n || slot[rec] == kNoRecord) return;
-  const uint8_t* s = reinterpret_cast<const uint8_t*>(src[rec]);
-  uint8_t* d = data + slot[rec] * row_bytes;
-  for (uint64_t o = (uint64_t)lane * VB; o < row_bytes; o += 64 * VB)
-    store_vec<VB>(d + o, load_vec<VB>(s + o));
+  const int64_t waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t rec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; rec < n; rec += waves) {
+    if (slot[rec] == kNoRecord) continue;
+    const uint8_t* s = reinterpret_cast<const uint8_t*>(src[rec]);
+    uint8_t* d = data + slot[rec] * row_bytes;
+    for (uint64_t o = (uint64_t)lane * VB; o < row_bytes; o += 64 * VB)
+      store_vec<VB>(d + o, load_vec<VB>(s + o));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -397,7 +702,9 @@ hipError_t launch_copy_rows(const uint32_t* num, uint32_t max_records, const uin
                             const uint64_t* src, int src_align, uint8_t* data, uint64_t row_bytes,
                             hipStream_t stream) {
   if (max_records == 0) return hipSuccess;
-  const dim3 grid(((uint64_t)max_records * 64 + 255) / 256);
+  // one wave per record, at most 8,192 workgroups (a record count known only
+  // on the device leaves most of an upper-bound grid idle)
+  const dim3 grid((unsigned)std::min<uint64_t>(((uint64_t)max_records * 64 + 255) / 256, 8192));
   const bool d16 = ((uintptr_t)data % 16 == 0) && row_bytes % 16 == 0;
   if (d16 && src_align % 16 == 0)
     hipLaunchKernelGGL(copy_rows_kernel<16>, grid, dim3(256), 0, stream, num, max_records, slot, src,
@@ -408,6 +715,22 @@ hipError_t launch_copy_rows(const uint32_t* num, uint32_t max_records, const uin
   else
     hipLaunchKernelGGL(copy_rows_kernel<1>, grid, dim3(256), 0, stream, num, max_records, slot, src,
                        data, row_bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_hash_insert(const HashInsertLaunch& h, const ReplaceLaunch& r, hipStream_t stream) {
+  if (h.n <= 0) return hipSuccess;
+  if (h.bits < 10 || h.bits > 30 || (1ll << h.bits) < 2 * h.n || h.n > 0xffffffffll) return hipErrorInvalidValue;
+  const int64_t slots = (1ll << h.bits) + 1;
+  hipLaunchKernelGGL(hins_clear_kernel, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, stream, h,
+                     r.rec_slot);
+  hipLaunchKernelGGL(hins_count_kernel, dim3((unsigned)((h.n + 1023) / 1024)), dim3(1024), 0, stream, h);
+  hipLaunchKernelGGL(hins_chain_kernel, dim3((unsigned)((h.n + 255) / 256)), dim3(256), 0, stream, h);
+  const unsigned rgrid = (unsigned)std::min<int64_t>((h.n * 8 + 255) / 256, 2048);
+  if (h.key_bytes == 4)
+    hipLaunchKernelGGL((hins_replace_kernel<int32_t, uint32_t>), dim3(rgrid), dim3(256), 0, stream, h, r);
+  else
+    hipLaunchKernelGGL((hins_replace_kernel<int64_t, uint64_t>), dim3(rgrid), dim3(256), 0, stream, h, r);
   return hipGetLastError();
 }
 

@@ -41,6 +41,37 @@ struct ReplaceLaunch {
 // rec_slot of a record position that holds no record
 constexpr uint64_t kNoRecord = ~0ull;
 
+// Hashed histogram of an insert into a large cache (modify.hip): the batch's
+// unique keys, counts and first positions from a hash table of 2^bits slots
+// (+1 for the key word ~0), each unique key chained into its set through the
+// table's per-set words, then the per-set replacement over the candidates
+// sorted into histogram order.  A set with more than kHashSetMax candidates
+// makes the call a no-op (counts[2] = 1) for the sorted histogram to redo.
+constexpr int kHashSetMax = 32;
+constexpr uint64_t kSetClean = 0x00000000ffffffffull;  // per-set word: no candidate, no chain
+struct HashInsertLaunch {
+  const void* keys;
+  int key_bytes;
+  int64_t n;
+  int bits;            // 2^bits >= 2n slots
+  uint64_t* tkey;      // 2^bits + 1 key words
+  uint32_t* tcount;    // 2^bits + 1 counts
+  uint32_t* tfirst;    // 2^bits + 1 first positions
+  uint32_t* ulist;     // n: the unique keys' slots, [0, counts[0])
+  uint32_t* unext;     // n: a unique key's successor in its set's chain
+  uint32_t* rsets;     // n: the touched sets, [0, counts[1])
+  uint32_t* counts;    // 4 words: unique keys, touched sets, overflow
+  uint64_t* set_word;  // num_sets words (candidates << 32 | chain head), kSetClean between inserts
+  uint64_t num_sets;
+  float norm;          // priority = float(count) * norm, norm = 1 / float(n)
+  const uint8_t* rows_base;
+  int64_t row_stride;
+  int by_key;          // source row: rows_base + key * stride (1) or + first position * stride (0)
+};
+// clear, count, chain, replace; the records (r.rec_*) are indexed by unique
+// key, [0, counts[0]), for the record kernels with num = counts
+hipError_t launch_hash_insert(const HashInsertLaunch& h, const ReplaceLaunch& r, hipStream_t stream);
+
 hipError_t launch_hist_prep(const void* keys, int key_bytes, int64_t n, uint64_t* k64, uint32_t* v,
                             hipStream_t stream);
 // heads[i] = 1 where a run of equal sorted keys starts; with span_part

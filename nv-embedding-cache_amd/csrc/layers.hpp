@@ -216,6 +216,10 @@ class GpuTable {
   void modify_rows(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
                    const uint8_t* d_vals, int64_t value_stride, bool accumulate, int dtype);
   void build_decay_table();
+  // the device-policy insert with the hashed histogram (large caches); false:
+  // a set had too many candidates and nothing changed (the sorted histogram redoes it)
+  bool hashed_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
+                     const uint8_t* rows, int64_t row_stride, bool from_uvm);
   int key_bytes_;
   GPUTableConfig cfg_;
   uint64_t num_sets_ = 0;
@@ -223,6 +227,10 @@ class GpuTable {
   void* tags_ = nullptr;
   float* counters_ = nullptr;
   int64_t* set_ts_ = nullptr;
+  // per-set words of the hashed histogram (device policy): kSetClean between
+  // inserts; an insert that failed part way leaves them to be cleaned first
+  uint64_t* set_word_ = nullptr;
+  bool set_words_dirty_ = false;
   int64_t global_ts_ = 0;
   // host policy state (modify_on_gpu = false): a copy of the device tags kept
   // in step by every modify, the way counters and the set timestamps

@@ -111,11 +111,94 @@ void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* key
     host_modify_insert(ctx, q.stream, n, keys, rows, cfg_.row_size_in_bytes, true);
 }
 
+// The hashed histogram (large caches): hash counts -> per-set chains -> per-set
+// replacement with the candidates sorted in their set -> invalidate; one
+// synchronization (where the sorted path also waits), which also reads the
+// overflow word; then the rows and tags.  Five launches before the wait and
+// two after, against about forty and two readbacks for the sorted histogram.
+bool GpuTable::hashed_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
+                             const uint8_t* rows, int64_t row_stride, bool from_uvm) {
+  if (set_words_dirty_) {  // an earlier insert stopped part way
+    NVE_HIP(launch_fill_u64(set_word_, (int64_t)num_sets_, kSetClean, s));
+    set_words_dirty_ = false;
+  }
+  int bits = 10;
+  while ((1ll << bits) < 2 * n) ++bits;
+  const size_t slots = ((size_t)1 << bits) + 1;
+  const size_t un = (size_t)n;
+  const size_t bytes = 12 * 256 + slots * (8 + 4 + 4) + un * (4 * 3 + 8 * 3) + 64 * 256;
+  uint8_t* p = static_cast<uint8_t*>(ctx.buffer("insert_hashed", bytes));
+  HashInsertLaunch h{};
+  h.keys = d_keys;
+  h.key_bytes = key_bytes_;
+  h.n = n;
+  h.bits = bits;
+  h.tkey = carve<uint64_t>(p, slots);
+  h.tcount = carve<uint32_t>(p, slots);
+  h.tfirst = carve<uint32_t>(p, slots);
+  h.ulist = carve<uint32_t>(p, un);
+  h.unext = carve<uint32_t>(p, un);
+  h.rsets = carve<uint32_t>(p, un);
+  h.counts = carve<uint32_t>(p, 4);
+  h.set_word = set_word_;
+  h.num_sets = num_sets_;
+  h.norm = 1.0f / (float)n;
+  h.rows_base = rows;
+  h.row_stride = row_stride;
+  h.by_key = from_uvm ? 1 : 0;
+  uint64_t* rec_slot = carve<uint64_t>(p, un);
+  int64_t* rec_tag = carve<int64_t>(p, un);
+  uint64_t* rec_src = carve<uint64_t>(p, un);
+  ReplaceLaunch r{};
+  r.tags = tags_;
+  r.counters = counters_;
+  r.set_ts = set_ts_;
+  r.global_ts = global_ts_;
+  r.decay_rate = decay_rate_;
+  r.decay_table = decay_table_;
+  r.decay_len = decay_len_;
+  r.num_sets = num_sets_;
+  r.sentinel = cfg_.invalid_key;
+  r.src_rows = from_uvm ? (uint64_t)cfg_.uvm_num_rows : 0;
+  r.max_records = (uint32_t)n;
+  r.rec_slot = rec_slot;
+  r.rec_tag = rec_tag;
+  r.rec_src = rec_src;
+  // the words are dirty from here until the replacement has run to its end
+  set_words_dirty_ = true;
+  NVE_HIP(launch_hash_insert(h, r, s));
+  set_words_dirty_ = false;  // stream order: the next insert's kernels follow these
+  const uint32_t* num = h.counts;  // records: one position per unique key
+  NVE_HIP(launch_invalidate(num, (uint32_t)n, rec_slot, tags_, key_bytes_, cfg_.invalid_key, s));
+  uint32_t* flags = static_cast<uint32_t*>(ctx.buffer("insert_hashed_flags", 64, true));
+  NVE_HIP(launch_small_read(flags, h.counts, 16, s));
+  // Lookups queued from here on see the invalidated tags; earlier ones may
+  // still read the replaced rows, so the copy waits for them
+  NVE_HIP(hipStreamSynchronize(s));
+  if (flags[2] != 0u) return false;  // a set past kHashSetMax candidates: nothing changed
+  lookups_->order_before(s);
+  uintptr_t align = (uintptr_t)rows | (uintptr_t)row_stride;
+  const int src_align = (align % 16 == 0) ? 16 : (align % 4 == 0) ? 4 : 1;
+  NVE_HIP(launch_copy_rows(num, (uint32_t)n, rec_slot, rec_src, src_align, data_,
+                           (uint64_t)cfg_.row_size_in_bytes, s));
+  NVE_HIP(launch_commit(num, (uint32_t)n, rec_slot, rec_tag, tags_, key_bytes_, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  return true;
+}
+
 void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* keys,
                              const uint8_t* rows, int64_t row_stride, bool from_uvm) {
   NVE_CHECK(n <= (int64_t)UINT32_MAX, "Too many keys for one insert");
   std::lock_guard<std::mutex> mk(modify_mu_);
   const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, s);
+  ++global_ts_;  // once per insert (ec_set_associative_device_modify.cuh:262)
+  // The hashed histogram where a set's candidates are few (no more sets than
+  // keys would crowd them), no candidate is cut (n <= max_modify_size) and
+  // histogram positions stay exact in float (n <= 2^24, as the sorted path's
+  // pass through the merge network as floats)
+  if (n >= 2 && n <= cfg_.max_modify_size && n <= (1ll << 24) && num_sets_ >= (uint64_t)n &&
+      hashed_insert(ctx, s, n, d_keys, rows, row_stride, from_uvm))
+    return;
 
   // ---- scratch (grow-only, per context) ----
   const size_t un = (size_t)n;
@@ -200,7 +283,6 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   NVE_HIP(launch_set_gather(sk, start, m, rset, roff, s));
 
   // ---- (3) replacement ----
-  ++global_ts_;  // once per insert (ec_set_associative_device_modify.cuh:262)
   ReplaceLaunch r{};
   r.rset = rset;
   r.roff = roff;
