@@ -20,6 +20,11 @@
 // four 8-bit passes, as many as 25 to 32 exact bits take) and learns whether
 // they did with the unique count; a batch whose keys differ higher up is
 // sorted again on its exact bits.
+//
+// Caches with at least as many sets as keys take the hashed histogram instead
+// of (1) and (2) (GpuTable::hashed_insert, modify.hip): hash counts, per-set
+// candidate chains and each set's candidates sorted into histogram order in
+// its replacement group; no readback, one wait.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -192,10 +197,10 @@ void GpuTable::modify_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, co
   std::lock_guard<std::mutex> mk(modify_mu_);
   const void* d_keys = device_input(ctx, "modify_keys", keys, (size_t)n * key_bytes_, s);
   ++global_ts_;  // once per insert (ec_set_associative_device_modify.cuh:262)
-  // The hashed histogram where a set's candidates are few (no more sets than
-  // keys would crowd them), no candidate is cut (n <= max_modify_size) and
-  // histogram positions stay exact in float (n <= 2^24, as the sorted path's
-  // pass through the merge network as floats)
+  // The hashed histogram where a set's candidates are few (fewer sets than
+  // keys would crowd them), none is cut (n <= max_modify_size) and the
+  // reference's histogram positions, which MergeBlock passes through a float,
+  // are exact (n <= 2^24), so that places within a set give the same result
   if (n >= 2 && n <= cfg_.max_modify_size && n <= (1ll << 24) && num_sets_ >= (uint64_t)n &&
       hashed_insert(ctx, s, n, d_keys, rows, row_stride, from_uvm))
     return;
