@@ -119,7 +119,7 @@ void GpuTable::insert_from_uvm(ExecutionContext& ctx, int64_t n, const void* key
 // The hashed histogram (large caches): hash counts -> per-set chains -> per-set
 // replacement with the candidates sorted in their set -> invalidate; one
 // synchronization (where the sorted path also waits), which also reads the
-// overflow word; then the rows and tags.  Five launches before the wait and
+// overflow word; then the rows and tags.  Six launches before the wait and
 // two after, against about forty and two readbacks for the sorted histogram.
 bool GpuTable::hashed_insert(ExecutionContext& ctx, hipStream_t s, int64_t n, const void* d_keys,
                              const uint8_t* rows, int64_t row_stride, bool from_uvm) {
