@@ -153,3 +153,32 @@ def test_hashed_set_past_its_candidate_limit_falls_back(key_bytes):
         ct.model.insert_keys(keys, values=vals.reshape(-1), value_stride=ct.width)
         assert_same_state(ct)
     ct.close()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_hashed_random_shapes(seed):
+    """Seeded random shapes: key width, row width, batch size, key spread and
+    repeats, values or backing rows, against the model over three inserts."""
+    rng = np.random.default_rng(1000 + seed)
+    key_bytes = int(rng.choice([4, 8]))
+    dim = int(rng.choice([4, 8, 16, 33]))
+    rows = int(rng.integers(500, 40000))
+    uvm = float_table(rng, rows, dim, O.F32)
+    ct = CachedTable(uvm, int(rng.choice([2, 4, 8])) * 1024 * 1024, key_bytes)
+    kdt = np.int64 if key_bytes == 8 else np.int32
+    for step in range(3):
+        n = int(rng.integers(2, min(ct.num_sets, 5000) + 1))
+        spread = int(rng.integers(2, 4 * rows))
+        keys = (rng.zipf(float(rng.uniform(1.05, 2.0)), size=n) % spread).astype(np.int64)
+        if rng.random() < 0.3:
+            keys = keys - spread // 2  # negative keys too
+        keys = keys.astype(kdt)
+        if rng.random() < 0.5:
+            _lib.call("nve_amd_table_insert_from_uvm", ct.table, ct.ctx, keys.size, vp(to_dev(keys)))
+            ct.model.insert_keys(keys, uvm=ct.uvm_np.reshape(-1))
+        else:
+            vals = rng.integers(0, 256, size=(keys.size, ct.width), dtype=np.uint8)
+            table_insert(ct, keys, vals, ct.width)
+            ct.model.insert_keys(keys, values=vals.reshape(-1), value_stride=ct.width)
+        assert_same_state(ct)
+    ct.close()

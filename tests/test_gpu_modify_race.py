@@ -11,7 +11,8 @@ which is what a lookup reading a way while an insert copies over it returns.
 
 The cache is small (64 sets) and each insert brings 1024 of 4096 keys, so
 nearly every insert evicts rows that concurrent lookups resolved a moment
-before."""
+before; the inserts also run against a 2048-set cache, where they take the
+hashed histogram."""
 import ctypes
 import threading
 
@@ -107,8 +108,11 @@ def run_race(modify_step, lookup, rounds=40, min_overlapped=5):
     return seen
 
 
-def test_table_find_racing_inserts():
-    rt = RaceTable()
+@pytest.mark.parametrize("sets", [64, 2048])
+def test_table_find_racing_inserts(sets):
+    """64 sets: the insert's sorted histogram; 2048 sets (more sets than the
+    1024 keys of an insert): its hashed histogram."""
+    rt = RaceTable(sets)
     rng = np.random.default_rng(5)
     keys = np.arange(NK, dtype=np.int64)
     d_keys = to_dev(keys)
