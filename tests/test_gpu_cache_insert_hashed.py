@@ -182,3 +182,94 @@ def test_hashed_random_shapes(seed):
             ct.model.insert_keys(keys, values=vals.reshape(-1), value_stride=ct.width)
         assert_same_state(ct)
     ct.close()
+
+
+def test_c3_shaped_batch_into_an_empty_large_cache():
+    """A C3-shaped batch (262,144 Zipf(1.2) keys over 4 M rows of 128 fp16,
+    permuted) inserted from the backing table into an empty cache of 2^20 sets
+    (the hashed path at full batch size; the oracle's model of a cache this
+    large would take gigabytes, so the result is held to what an empty cache
+    fixes): every set with at most 8 distinct candidates holds all of them, a
+    fuller set holds 8 of them and none it left out has a higher count, each
+    resident way's counter is its key's priority float(count) * (1 / float(n))
+    bit for bit, touched sets carry timestamp 1 and the others nothing; then,
+    with every backing row changed on the host, lookups return the old row for
+    exactly the resident keys."""
+    import ctypes
+    rows, width, n = 4_000_000, 256, 262144
+    ns_want = 1 << 20
+    L = _lib.load()
+    host = torch.arange(rows * (width // 4), dtype=torch.int32).view(torch.uint8).pin_memory()
+    cfg = L.nve_gpu_table_config_default()
+    cfg.cache_size = ns_want * 2144  # 64 B of tags, 2 KiB of rows, 32 B of counters per set
+    cfg.row_size_in_bytes = width
+    cfg.value_dtype = _lib.DT_F16
+    cfg.uvm_table = host.data_ptr()
+    cfg.uvm_num_rows = rows
+    table = ctypes.c_void_p()
+    _lib.call("nve_gpu_table_create", ctypes.byref(table), _lib.KEY_INT64, ctypes.byref(cfg), None)
+    ctx = ctypes.c_void_p()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.call("nve_table_create_execution_context", table, ctypes.byref(ctx), s, s, None, None)
+    try:
+        nsv = ctypes.c_int64()
+        _lib.call("nve_amd_gpu_table_num_sets", table, ctypes.byref(nsv))
+        ns = nsv.value
+        assert ns == ns_want
+        rng = np.random.default_rng(2024)
+        perm = rng.permutation(rows)
+        keys = perm[O.power_law(rng.random(n), 1, rows, 1.2).astype(np.int64) - 1].astype(np.int64)
+        d_keys = to_dev(keys)
+        _lib.call("nve_amd_table_insert_from_uvm", table, ctx, n, vp(d_keys))
+        _lib.call("nve_context_wait", ctx)
+
+        tags = np.zeros(ns * 8, np.int64)
+        ctr = np.zeros(ns * 8, np.float32)
+        ts = np.zeros(ns, np.int64)
+        gts = ctypes.c_int64()
+        _lib.call("nve_amd_gpu_table_export_state", table, tags.ctypes.data_as(ctypes.c_void_p),
+                  ctr.ctypes.data_as(ctypes.c_void_p), ts.ctypes.data_as(ctypes.c_void_p), ctypes.byref(gts))
+        assert gts.value == 1
+
+        uk, cnt = np.unique(keys, return_counts=True)
+        useti = uk % ns
+        norm = np.float32(1.0) / np.float32(n)
+        prio = cnt.astype(np.float32) * norm
+        occ = np.nonzero(tags != -1)[0]
+        res_set = occ // 8
+        res_key = tags[occ] * ns + res_set
+        # residents are candidates of their set, each once
+        pos = np.searchsorted(uk, res_key)
+        assert np.all(pos < uk.size) and np.array_equal(uk[pos], res_key)
+        assert np.unique(res_key).size == res_key.size
+        assert np.array_equal(ctr[occ].view(np.uint32), prio[pos].view(np.uint32))
+        assert np.all(ctr[tags == -1] == 0.0)
+        touched = np.zeros(ns, bool)
+        touched[useti] = True
+        assert np.array_equal(ts, touched.astype(np.int64))
+        # per set: all candidates when at most 8, else 8 with no left-out count above a resident's
+        per_set = np.bincount(useti, minlength=ns)
+        held = np.bincount(res_set, minlength=ns)
+        assert np.array_equal(held, np.minimum(per_set, 8))
+        resident = np.zeros(uk.size, bool)
+        resident[pos] = True
+        full = np.nonzero(per_set > 8)[0]
+        for st in full:
+            idx = np.nonzero(useti == st)[0]
+            assert cnt[idx][resident[idx]].min() >= cnt[idx][~resident[idx]].max()
+
+        # backing rows changed on the host: resident keys still return the old row
+        host.view(torch.int32).bitwise_xor_(0x5A5A5A5A)
+        out = torch.zeros((uk.size, width), dtype=torch.uint8, device="cuda")
+        d_uk = to_dev(uk)
+        _lib.call("nve_table_find", table, ctx, uk.size, vp(d_uk), None, width, vp(out), None)
+        _lib.call("nve_context_wait", ctx)
+        torch.cuda.synchronize()
+        got = out.cpu().view(torch.int32).numpy().reshape(uk.size, width // 4)
+        base = (uk[:, None] * (width // 4) + np.arange(width // 4)[None, :]).astype(np.int32)
+        want = np.where(resident[:, None], base, base ^ np.int32(0x5A5A5A5A))
+        assert np.array_equal(got, want)
+    finally:
+        _lib.call("nve_context_wait", ctx)
+        _lib.call("nve_context_destroy", ctx)
+        _lib.call("nve_table_destroy", table)
