@@ -162,6 +162,11 @@ int table_through_buffer_ptr(hipStream_t s, const std::vector<int64_t>& keys, co
   if (dk == nullptr || dk == keys.data() || host_keys->get_last_access() != hipMemoryTypeDevice)
     return fail("access_buffer did not stage the keys on the device");
   auto kb = std::make_shared<nve::BufferWrapper<const void>>(tctx, "dkeys", dk, n * 8);
+  // and back: a host copy of the device keys, made once (a const buffer)
+  const void* hk = kb->access_buffer(hipMemoryTypeHost, true, s);
+  if (hk == nullptr || hk == dk || std::memcmp(hk, keys.data(), (size_t)n * 8) != 0 ||
+      kb->get_buffer(hipMemoryTypeDevice) != dk || kb->access_buffer(hipMemoryTypeHost, true, s) != hk)
+    return fail("access_buffer did not stage the device keys on the host");
   auto rows = std::make_shared<nve::BufferWrapper<const void>>(tctx, "rows", want_g.data(), (size_t)(n * dim) * 4);
   gt->insert(tctx, n, kb, dim * 4, dim * 4, rows);
   std::vector<float> vals((size_t)(n * dim));
