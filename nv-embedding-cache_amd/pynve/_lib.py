@@ -3,7 +3,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "libnve_amd.so")
+# NVE_AMD_LIB: another build of the library (e.g. the Makefile's `asan` target)
+LIB_PATH = os.environ.get("NVE_AMD_LIB") or os.path.join(os.path.dirname(_HERE), "libnve_amd.so")
 
 # nve_status_t
 SUCCESS, INVALID_ARGUMENT, HIP_ERROR, RUNTIME, NOT_IMPLEMENTED, OUT_OF_MEMORY = range(6)
