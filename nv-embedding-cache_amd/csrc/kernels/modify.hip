@@ -425,7 +425,7 @@ __global__ __launch_bounds__(1024) void hins_count_kernel(HashInsertLaunch a) {
     atomicMin(&lfirst[ls], (uint32_t)i);
   } else if (in) {  // the key word kHashEmpty: its own slot
     atomicAdd(&a.tcount[special], 1u);
-    atomicMin(&a.tfirst[special], (uint32_t)i);
+    if (!a.by_key) atomicMin(&a.tfirst[special], (uint32_t)i);
     won = atomicCAS(reinterpret_cast<unsigned long long*>(a.tkey + special), (unsigned long long)kHashEmpty,
                     0ull) == (unsigned long long)kHashEmpty;
   }
@@ -434,7 +434,8 @@ __global__ __launch_bounds__(1024) void hins_count_kernel(HashInsertLaunch a) {
   if (first) {
     gs = hins_claim(a.tkey, k, a.bits, &won);
     atomicAdd(&a.tcount[gs], lcnt[ls]);
-    atomicMin(&a.tfirst[gs], lfirst[ls]);
+    // the first position names the source row only for rows given with the keys
+    if (!a.by_key) atomicMin(&a.tfirst[gs], lfirst[ls]);
   }
   wg_append(won, gs, &a.counts[0], a.ulist, s_wave, &s_base);
 }
