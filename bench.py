@@ -767,11 +767,51 @@ def run_workload(args, torch, _lib):
                 torch.cuda.synchronize()
                 if i:  # the first call sizes its scratch
                     ins.append((time.perf_counter() - t0) * 1e6)
-            _lib.call("nve_context_destroy", tctx)
             ins.sort()
             cfg_out["insert_us"] = {"median": round(ins[len(ins) // 2], 1), "min": round(ins[0], 1),
                                     "max": round(ins[-1], 1), "calls": len(ins), "keys_per_call": nkeys}
             log(f"c3: insert of a {nkeys}-key batch: median {ins[len(ins) // 2]:.1f} us over {len(ins)} calls")
+            # the insert of a collection of plain lookups: the same histogram and
+            # replacement, rows copied from the lookups' output kept in HBM
+            # (layer_utils.cpp:187-193, 266-267) instead of read over the host link
+            rows_buf = torch.empty((nkeys, width), dtype=torch.uint8, device="cuda")
+            ins_rows = []
+            for i in range(args.c3_insert_steps + 1):
+                b = batches[(20 + nt + i) % len(batches)]
+                bp = ctypes.c_void_p(b.data_ptr())
+                _lib.call("nve_table_find", table, tctx, nkeys, bp, None, width,
+                          ctypes.c_void_p(rows_buf.data_ptr()), None)
+                _lib.call("nve_context_wait", tctx)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                _lib.call("nve_table_insert", table, tctx, nkeys, bp, width, width,
+                          ctypes.c_void_p(rows_buf.data_ptr()))
+                _lib.call("nve_context_wait", tctx)
+                torch.cuda.synchronize()
+                if i:
+                    ins_rows.append((time.perf_counter() - t0) * 1e6)
+            _lib.call("nve_context_destroy", tctx)
+            # the collection's own cost: one device copy of the batch's output rows
+            kept = torch.empty_like(rows_buf)
+            cps = []
+            for i in range(6):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                kept.copy_(rows_buf)
+                e1.record()
+                e1.synchronize()
+                if i:
+                    cps.append(e0.elapsed_time(e1) * 1e3)
+            del rows_buf, kept
+            ins_rows.sort()
+            cps.sort()
+            cfg_out["insert_from_lookup_rows_us"] = {
+                "median": round(ins_rows[len(ins_rows) // 2], 1), "min": round(ins_rows[0], 1),
+                "max": round(ins_rows[-1], 1), "calls": len(ins_rows), "keys_per_call": nkeys,
+                "collect_copy_us": round(cps[len(cps) // 2], 1)}
+            log(f"c3: insert of a {nkeys}-key batch from lookup rows in HBM: median "
+                f"{ins_rows[len(ins_rows) // 2]:.1f} us over {len(ins_rows)} calls; collecting the batch's "
+                f"rows (one device copy) {cps[len(cps) // 2]:.1f} us")
         if args.c3_update_steps > 0 and not args.c3_resident:
             # the cache's update and update_accumulate of a whole batch (every key
             # resident) on a cache-only table of the same rows (4 GiB, no backing

@@ -306,12 +306,20 @@ class LinearUVMEmbeddingLayer : public EmbeddingLayer {
   std::shared_ptr<LookupStreams> lookup_streams() const override { return table_->lookup_streams(); }
 
  private:
-  void auto_insert(ExecutionContext& ctx, int64_t n, const void* d_keys, float hitrate);
+  void auto_insert(ExecutionContext& ctx, int64_t n, const void* d_keys, const void* d_out,
+                   int64_t out_stride, bool from_uvm, float hitrate);
+  void reset_collection();  // with collect_mu_ held
+  struct CollectedRows;     // device copy of the collected lookups' output rows
   LinearUVMLayerConfig cfg_;
   std::shared_ptr<GpuTable> table_;
   std::mutex collect_mu_;
   std::vector<uint8_t> collected_;  // keys gathered for the next insert
   int64_t collected_n_ = 0;
+  // A collection of plain lookups keeps their output rows and inserts those;
+  // one that a pooled lookup joined inserts from the backing table.
+  bool collection_is_uvm_ = false;
+  int64_t collected_stride_ = 0;                   // output stride of a collection of rows
+  std::shared_ptr<CollectedRows> collected_rows_;  // shared with the insert task that reads it
   int64_t insert_wait_ = 0;                       // lookups to skip before the next collection
   std::shared_ptr<std::atomic<bool>> in_flight_;  // an auto-insert task is running
 };

@@ -242,6 +242,10 @@ void LinearUVMEmbeddingLayer::update(ExecutionContext& ctx, int64_t n, const voi
   check_update_args(n, keys, values, value_stride, value_size);
   NVE_CHECK_ARG(value_size == table_->config().row_size_in_bytes, "Invalid value size");
   NVE_CHECK_ARG(table_id < num_tables(), "Invalid table_id");
+  {
+    std::lock_guard<std::mutex> lk(collect_mu_);
+    reset_collection();  // collected lookup rows may predate the new values
+  }
   table_->update(ctx, n, keys, value_stride, value_size, values);
 }
 
@@ -251,6 +255,10 @@ void LinearUVMEmbeddingLayer::accumulate(ExecutionContext& ctx, int64_t n, const
   check_update_args(n, keys, values, value_stride, value_size);
   NVE_CHECK_ARG(value_size == table_->config().row_size_in_bytes, "Invalid value size");
   NVE_CHECK_ARG(table_id < num_tables(), "Invalid table_id");
+  {
+    std::lock_guard<std::mutex> lk(collect_mu_);
+    reset_collection();  // collected lookup rows may predate the new values
+  }
   table_->update_accumulate(ctx, n, keys, value_stride, value_size, values, value_type);
 }
 

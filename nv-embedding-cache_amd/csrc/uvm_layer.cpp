@@ -6,7 +6,10 @@
 // the hit rate, then hand the keys to the auto-insert protocol
 // (layer_utils.cpp:94-275): once the heuristic fires, keys are collected
 // until min_insert_size_gpu of them exist, and the insert runs as a task on
-// the context's thread pool, promoting the rows from the backing table.
+// the context's thread pool.  Plain lookups also keep their output rows (a
+// device-to-device copy) and the insert takes them from HBM; a pooled lookup
+// has no per-key rows, so a collection it joins promotes the rows from the
+// backing table (linear_embedding_layer.cu:197-206).
 #include <climits>
 #include <cstring>
 
@@ -102,37 +105,85 @@ void LinearUVMEmbeddingLayer::lookup(ExecutionContext& ctx, int64_t num_keys, co
     const float hitrate =
         num_keys > 0 ? 1.0f - (float)misses / (float)num_keys : 1.0f;
     if (hitrates) *hitrates = hitrate;
-    if (!never && num_keys > 0) auto_insert(ctx, num_keys, d_keys, hitrate);
+    if (!never && num_keys > 0) auto_insert(ctx, num_keys, d_keys, d_out, output_stride, pooled, hitrate);
   }
 }
 
-// Auto-insert: collect keys from lookups once the heuristic fires; insert
-// from the backing table when min_insert_size_gpu keys are collected.
+struct LinearUVMEmbeddingLayer::CollectedRows {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  explicit CollectedRows(size_t b) : bytes(b) { NVE_HIP(hipMalloc(&ptr, b)); }
+  ~CollectedRows() { (void)hipFree(ptr); }
+  CollectedRows(const CollectedRows&) = delete;
+  CollectedRows& operator=(const CollectedRows&) = delete;
+};
+
+void LinearUVMEmbeddingLayer::reset_collection() {
+  collected_.clear();
+  collected_n_ = 0;
+  collection_is_uvm_ = false;
+}
+
+// Auto-insert (layer_utils.cpp:94-143): collect keys, and the output rows of
+// plain lookups, once the heuristic fires; insert when min_insert_size_gpu
+// keys are collected.
 void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, const void* d_keys,
+                                          const void* d_out, int64_t out_stride, bool from_uvm,
                                           float hitrate) {
   std::unique_lock<std::mutex> lk(collect_mu_, std::try_to_lock);
   if (!lk.owns_lock()) return;  // an insert is being collected or launched elsewhere
   if (in_flight_ && in_flight_->load()) return;  // the previous insert still runs
   const int64_t min_size = cfg_.min_insert_size_gpu > 0 ? cfg_.min_insert_size_gpu : 1;
-  if (collected_n_ == 0) {
+  if (collected_n_ > 0) {
+    // a pooled lookup joining a collection of rows turns it into one that
+    // promotes from the backing table for good, and its rows are dropped
+    collection_is_uvm_ = collection_is_uvm_ || from_uvm;
+    NVE_CHECK(collection_is_uvm_ || out_stride == collected_stride_,
+              "Output stride must be fixed during accumulation");
+  } else {
     // min_insert_freq_gpu lookups pass between inserts (layer_utils.cpp:120-131)
     if (--insert_wait_ >= 0) return;
     insert_wait_ = 0;
     if (!cfg_.insert_heuristic->insert_needed(hitrate, 0)) return;
+    collection_is_uvm_ = from_uvm;
+    collected_stride_ = out_stride;
   }
   const int64_t total = collected_n_ == 0 ? std::max(n, min_size) : min_size;
   const int64_t part = std::min(n, total - collected_n_);
   if (part <= 0) return;
+  const hipStream_t s = ctx.lookup_stream();
+  const size_t stride = (size_t)collected_stride_;
+  uint8_t* rows = nullptr;
+  if (!collection_is_uvm_) {
+    // sized for the whole collection when it starts, so later parts never
+    // move it; an insert task still holding the previous buffer keeps it
+    if (collected_n_ == 0 &&
+        (!collected_rows_ || collected_rows_.use_count() > 1 || collected_rows_->bytes < (size_t)total * stride))
+      collected_rows_ = std::make_shared<CollectedRows>((size_t)total * stride);
+    rows = static_cast<uint8_t*>(collected_rows_->ptr);
+    NVE_HIP(hipMemcpyAsync(rows + (size_t)collected_n_ * stride, d_out, (size_t)part * stride,
+                           hipMemcpyDeviceToDevice, s));
+  }
   collected_.resize((size_t)(collected_n_ + part) * key_bytes_);
   NVE_HIP(hipMemcpyAsync(collected_.data() + (size_t)collected_n_ * key_bytes_, d_keys,
-                         (size_t)part * key_bytes_, hipMemcpyDefault, ctx.lookup_stream()));
-  NVE_HIP(hipStreamSynchronize(ctx.lookup_stream()));
-  // keys outside the backing table (no default row configured) cannot be
-  // inserted from it: drop them here
+                         (size_t)part * key_bytes_, hipMemcpyDefault, s));
+  NVE_HIP(hipStreamSynchronize(s));
+  // keys outside the backing table (no default row configured) have no row
+  // to promote and no defined lookup row: drop them here, with their rows
   {
-    const uint64_t rows = (uint64_t)table_->config().uvm_num_rows;
+    const uint64_t num_rows = (uint64_t)table_->config().uvm_num_rows;
     uint8_t* base = collected_.data() + (size_t)collected_n_ * key_bytes_;
     int64_t kept = 0;
+    int64_t run = -1;  // first part position of the current run of kept keys
+    // a run that moved down gets its rows again from the lookup's output
+    auto flush = [&](int64_t end) {
+      const int64_t len = end - run;
+      if (rows && run >= 0 && kept - len != run)
+        NVE_HIP(hipMemcpyAsync(rows + (size_t)(collected_n_ + kept - len) * stride,
+                               static_cast<const uint8_t*>(d_out) + (size_t)run * stride,
+                               (size_t)len * stride, hipMemcpyDeviceToDevice, s));
+      run = -1;
+    };
     for (int64_t i = 0; i < part; ++i) {
       int64_t k;
       if (key_bytes_ == 4) {
@@ -142,10 +193,16 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
       } else {
         std::memcpy(&k, base + (size_t)i * 8, 8);
       }
-      if ((uint64_t)k >= rows) continue;
+      if ((uint64_t)k >= num_rows) {
+        flush(i);
+        continue;
+      }
       if (kept != i) std::memmove(base + (size_t)kept * key_bytes_, base + (size_t)i * key_bytes_, key_bytes_);
+      if (run < 0) run = i;
       ++kept;
     }
+    flush(part);
+    if (rows && kept != part) NVE_HIP(hipStreamSynchronize(s));
     collected_n_ += kept;
     collected_.resize((size_t)collected_n_ * key_bytes_);
   }
@@ -153,7 +210,9 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
   std::vector<uint8_t> keys;
   keys.swap(collected_);
   const int64_t nk = collected_n_;
+  std::shared_ptr<CollectedRows> data = collection_is_uvm_ ? nullptr : collected_rows_;
   collected_n_ = 0;
+  collection_is_uvm_ = false;
   // the insert itself runs as a pool task; wait() on the context joins it
   insert_wait_ = cfg_.min_insert_freq_gpu;
   if (!in_flight_) in_flight_ = std::make_shared<std::atomic<bool>>(false);
@@ -161,13 +220,23 @@ void LinearUVMEmbeddingLayer::auto_insert(ExecutionContext& ctx, int64_t n, cons
   std::shared_ptr<GpuTable> table = table_;
   std::shared_ptr<std::atomic<bool>> flag = in_flight_;
   ExecutionContext* c = &ctx;
-  NVE_LOG_PERF("auto-insert of ", nk, " keys launched (hit rate ", hitrate, ")");
-  ctx.add_pending(ctx.pool().submit([table, c, nk, flag, keys = std::move(keys)]() {
+  NVE_LOG_PERF("auto-insert of ", nk, " keys launched (hit rate ", hitrate, ", rows from the ",
+               data ? "lookups" : "backing table", ")");
+  ctx.add_pending(ctx.pool().submit([table, c, nk, flag, data, stride, keys = std::move(keys)]() mutable {
+    // the task (with its captures) lives on in the context's future until
+    // wait(): hand the rows back to the next collection before the flag drops
     struct Done {
       std::atomic<bool>* f;
-      ~Done() { f->store(false); }
-    } done{flag.get()};
-    table->insert_from_uvm(*c, nk, keys.data());
+      std::shared_ptr<CollectedRows>* d;
+      ~Done() {
+        d->reset();
+        f->store(false);
+      }
+    } done{flag.get(), &data};
+    if (data)
+      table->insert(*c, nk, keys.data(), (int64_t)stride, table->config().row_size_in_bytes, data->ptr);
+    else
+      table->insert_from_uvm(*c, nk, keys.data());
   }));
 }
 
@@ -177,16 +246,14 @@ void LinearUVMEmbeddingLayer::insert(ExecutionContext& ctx, int64_t n, const voi
   NVE_CHECK_ARG(table_id <= 0, "Invalid table id ", table_id);
   {
     std::lock_guard<std::mutex> lk(collect_mu_);
-    collected_.clear();
-    collected_n_ = 0;
+    reset_collection();
   }
   table_->insert(ctx, n, keys, value_stride, value_size, values);
 }
 
 void LinearUVMEmbeddingLayer::clear(ExecutionContext& ctx) {
   std::lock_guard<std::mutex> lk(collect_mu_);
-  collected_.clear();
-  collected_n_ = 0;
+  reset_collection();
   table_->clear(ctx);
 }
 
@@ -194,8 +261,7 @@ void LinearUVMEmbeddingLayer::erase(ExecutionContext& ctx, int64_t n, const void
                                     int64_t table_id) {
   NVE_CHECK_ARG(table_id <= 0, "Invalid table id ", table_id);
   std::lock_guard<std::mutex> lk(collect_mu_);
-  collected_.clear();
-  collected_n_ = 0;
+  reset_collection();
   table_->erase(ctx, n, keys);
 }
 
