@@ -106,3 +106,41 @@ def test_unknown_kernel_mode_is_rejected():
     t = ctypes.c_void_p()
     with pytest.raises(_lib.InvalidArgument, match="kernel_mode_type"):
         _lib.call("nve_gpu_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(cfg), None)
+
+
+@pytest.mark.parametrize("mode", [LOOKUP, SORT, PIPE])
+@pytest.mark.parametrize("key_bytes", [4, 8])
+@pytest.mark.parametrize("modify_on_gpu", [False, True])
+def test_mode_boundaries_empty_all_misses_all_hits(mode, key_bytes, modify_on_gpu):
+    """pipeline_gather_boundary_tests.cu:147-205 for every lookup mode: an empty
+    lookup writes nothing and counts nothing, 500 keys of an empty cache all
+    miss and read the backing rows, and 32 inserted keys all hit.  The
+    backing row of key i holds bytes (i + j) % 256; the inserted rows hold
+    their complement, so a hit is seen to come from the cache."""
+    rows, width = 100000, 32
+    uvm = ((np.arange(rows)[:, None] + np.arange(width)[None, :]) % 256).astype(np.uint8)
+    params = (ctypes.c_uint64 * 2)(4096, 4)
+    ct = CachedTable(uvm, 1 << 20, key_bytes, value_dtype=_lib.DT_F32, kernel_mode_type=mode,
+                     kernel_mode_value=ctypes.addressof(params) if mode == PIPE else 0,
+                     modify_on_gpu=modify_on_gpu)
+    kdt = np.int64 if key_bytes == 8 else np.int32
+    empty = torch.zeros(1, dtype=torch.int64 if key_bytes == 8 else torch.int32, device="cuda")
+    out = torch.full((1, width), 0x5A, dtype=torch.uint8, device="cuda")
+    _lib.call("nve_table_reset_lookup_counter", ct.table, ct.ctx)
+    _lib.call("nve_table_find", ct.table, ct.ctx, 0, vp(empty), None, width, vp(out), None)
+    cnt = ctypes.c_int64()
+    _lib.call("nve_table_get_lookup_counter", ct.table, ct.ctx, ctypes.byref(cnt))
+    assert cnt.value == 0 and bool((out == 0x5A).all())
+
+    keys = np.arange(500, dtype=kdt)
+    got, misses = run_find(ct, keys, width)
+    assert misses == 500
+    assert np.array_equal(got, uvm[:500])
+
+    hot = np.arange(32, dtype=kdt)
+    from test_gpu_cache_insert import table_insert
+    table_insert(ct, hot, ~uvm[:32], width)
+    got, misses = run_find(ct, hot, width)
+    assert misses == 0
+    assert np.array_equal(got, ~uvm[:32])
+    ct.close()
