@@ -329,10 +329,16 @@ nve_status_t nve_table_destroy(nve_table_t table) {
   if (!table || (!table->ptr && !table->host) || !ctx || !ctx->ptr)          \
     return set_error(NVE_ERROR_INVALID_ARGUMENT, "table and ctx must not be NULL");
 
+// keys is the one buffer these calls cannot do without (nve_c_api_tables.cpp:97-99)
+#define NEED_KEYS                                                            \
+  if (n > 0 && !keys)                                                        \
+    return set_error(NVE_ERROR_INVALID_ARGUMENT, "keys must not be NULL when n > 0");
+
 nve_status_t nve_table_find(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys,
                             uint64_t* hit_mask, int64_t value_stride, void* values,
                             int64_t* value_sizes) {
   NEED_TABLE_CTX
+  NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_find");
   if (table->host)
@@ -346,6 +352,7 @@ nve_status_t nve_table_find(nve_table_t table, nve_context_t ctx, int64_t n, con
 nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys,
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
+  NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_insert");
   if (table->host) return NVE_SUCCESS;  // a linear host table holds every row: no effect
@@ -357,6 +364,7 @@ nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, c
 nve_status_t nve_table_update(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys,
                               int64_t value_stride, int64_t value_size, const void* values) {
   NEED_TABLE_CTX
+  NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_update");
   if (table->host)
@@ -372,6 +380,7 @@ nve_status_t nve_table_update_accumulate(nve_table_t table, nve_context_t ctx, i
                                          int64_t value_size, const void* values,
                                          nve_data_type_t value_type) {
   NEED_TABLE_CTX
+  NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_update_accumulate");
   if (table->host)
@@ -396,6 +405,7 @@ nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
 
 nve_status_t nve_table_erase(nve_table_t table, nve_context_t ctx, int64_t n, const void* keys) {
   NEED_TABLE_CTX
+  NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_erase");
   if (table->host) return NVE_SUCCESS;  // no effect on a linear host table

@@ -33,7 +33,8 @@ GpuTable::GpuTable(int key_bytes, const GPUTableConfig& cfg) : key_bytes_(key_by
   NVE_CHECK(cfg_.uvm_table == nullptr || cfg_.uvm_num_rows > 0,
             "uvm_num_rows must be set to the number of rows in uvm_table");
   NVE_CHECK(cfg_.max_modify_size > 0, "max_modify_size must be positive");
-  NVE_CHECK_ARG(cfg_.kernel_mode_type <= 3, "Unsupported kernel_mode_type ", cfg_.kernel_mode_type);
+  // an unknown kernel_mode_type is accepted here and reported as not
+  // implemented by the first lookup that needs a mode (gpu_table.cu:271-287)
   if (cfg_.kernel_mode_type == 3 && cfg_.kernel_mode_value != 0) {
     // PipelineGather: kernel_mode_value points at {task_size, num_aux_streams}
     // (GatherKernelPipelineParams, pipeline_gather.cuh:33-36), read once here

@@ -57,11 +57,13 @@ std::string cat(const T&... parts) {
   } while (0)
 #define NVE_NOT_IMPLEMENTED(...) \
   throw ::nve_amd::Error(NVE_ERROR_NOT_IMPLEMENTED, ::nve_amd::cat(__VA_ARGS__))
+// A failed call also resets the thread's last-error state, so that a later
+// launch check (hipGetLastError after a kernel launch) does not report it again.
 #define NVE_HIP(expr)                                                                        \
   do {                                                                                       \
     const hipError_t e_ = (expr);                                                            \
     if (e_ != hipSuccess)                                                                    \
-      throw ::nve_amd::Error(e_ == hipErrorOutOfMemory ? NVE_ERROR_OUT_OF_MEMORY : NVE_ERROR_CUDA, \
+      (void)hipGetLastError(), throw ::nve_amd::Error(e_ == hipErrorOutOfMemory ? NVE_ERROR_OUT_OF_MEMORY : NVE_ERROR_CUDA, \
                              ::nve_amd::cat(#expr, ": ", hipGetErrorName(e_), " (",              \
                                             hipGetErrorString(e_), ")"));                    \
   } while (0)

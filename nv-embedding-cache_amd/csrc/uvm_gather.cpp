@@ -97,7 +97,8 @@ GpuTable::UvmMode GpuTable::uvm_mode(int64_t n) const {
     }
     case 1: return UvmMode::Lookup;
     case 2: return UvmMode::SortGather;
-    default: return UvmMode::PipelineGather;
+    case 3: return UvmMode::PipelineGather;
+    default: NVE_NOT_IMPLEMENTED("Unsupported kernel_mode_type ", cfg_.kernel_mode_type);
   }
 }
 

@@ -98,14 +98,37 @@ def test_pipeline_default_params_and_all_misses():
     ct.close()
 
 
-def test_unknown_kernel_mode_is_rejected():
+def test_unknown_kernel_mode_is_not_implemented_at_the_lookup():
+    """c_api_boundary_test.cpp:103-131: a table with an unknown
+    kernel_mode_type is created, and its first lookup over the backing table
+    reports NVE_ERROR_NOT_IMPLEMENTED (get_kernel_mode, gpu_table.cu:271-287);
+    a table without a backing table never asks for a mode."""
     L = _lib.load()
-    cfg = L.nve_gpu_table_config_default()
-    cfg.cache_size, cfg.row_size_in_bytes, cfg.value_dtype = 1 << 20, 64, _lib.DT_F32
-    cfg.kernel_mode_type = 7
-    t = ctypes.c_void_p()
-    with pytest.raises(_lib.InvalidArgument, match="kernel_mode_type"):
+    h_uvm = torch.zeros(16 * 16, dtype=torch.float32).pin_memory()
+    for with_uvm in (True, False):
+        cfg = L.nve_gpu_table_config_default()
+        cfg.cache_size, cfg.row_size_in_bytes, cfg.value_dtype = 1 << 20, 64, _lib.DT_F32
+        cfg.kernel_mode_type = 99
+        if with_uvm:
+            cfg.uvm_table, cfg.uvm_num_rows = h_uvm.data_ptr(), 16
+        t = ctypes.c_void_p()
         _lib.call("nve_gpu_table_create", ctypes.byref(t), _lib.KEY_INT64, ctypes.byref(cfg), None)
+        ctx = ctypes.c_void_p()
+        s = stream_ptr()
+        _lib.call("nve_table_create_execution_context", t, ctypes.byref(ctx), s, s, None, None)
+        keys = torch.zeros(1, dtype=torch.int64, device="cuda")
+        out = torch.zeros(64, dtype=torch.uint8, device="cuda")
+        mask = torch.zeros(1, dtype=torch.int64, device="cuda")
+        st = L.nve_table_find(t, ctx, 1, vp(keys), vp(mask), 64, vp(out), None)
+        if with_uvm:
+            assert st == _lib.NOT_IMPLEMENTED, _lib.last_error()
+            assert "kernel_mode_type" in _lib.last_error()
+        else:
+            assert st == _lib.SUCCESS
+            assert int(mask.cpu()[0]) == 0  # an empty cache: a miss
+        torch.cuda.synchronize()
+        _lib.call("nve_context_destroy", ctx)
+        _lib.call("nve_table_destroy", t)
 
 
 @pytest.mark.parametrize("mode", [LOOKUP, SORT, PIPE])
