@@ -193,12 +193,23 @@ nve_status_t nve_abi_version(int32_t* major, int32_t* minor) {
 }
 
 // ---- thread pool ----
-nve_status_t nve_thread_pool_create(nve_thread_pool_t* out, const char* json_config) {
-  if (!out) return set_error(NVE_ERROR_INVALID_ARGUMENT, "out must not be NULL");
-  C_TRY
-  const int64_t n = json_int_field(json_config ? json_config : "{}", "num_workers", 0);
+// thread_pool.cpp:46-68: "simple" (the default) and "numa" name the reference's
+// implementations; a NUMA-pinned pool is not part of this build, so "numa"
+// makes the same worker pool as "simple".
+static int64_t thread_pool_workers(const char* json_config) {
+  const std::string impl = json_string_field(json_config, "implementation", "simple");
+  NVE_CHECK(impl == "simple" || impl == "numa", "Thread pool implementation '", impl, "' not found!");
+  const int64_t n = json_int_field(json_config, "num_workers", 0);
   NVE_CHECK_ARG(n >= 0, "num_workers must not be negative");
-  *out = new nve_thread_pool_s{std::make_shared<ThreadPool>(n)};
+  return n;
+}
+
+nve_status_t nve_thread_pool_create(nve_thread_pool_t* out, const char* json_config) {
+  if (!out || !json_config)
+    return set_error(NVE_ERROR_INVALID_ARGUMENT, "out and json_config must not be NULL");
+  *out = nullptr;
+  C_TRY
+  *out = new nve_thread_pool_s{std::make_shared<ThreadPool>(thread_pool_workers(json_config))};
   return NVE_SUCCESS;
   C_CATCH
 }
@@ -221,7 +232,7 @@ nve_status_t nve_thread_pool_num_workers(nve_thread_pool_t pool, int64_t* out) {
 nve_status_t nve_configure_default_thread_pool(const char* json_config) {
   if (!json_config) return set_error(NVE_ERROR_INVALID_ARGUMENT, "json_config must not be NULL");
   C_TRY
-  ThreadPool::configure_default(json_int_field(json_config, "num_workers", 0));
+  ThreadPool::configure_default(thread_pool_workers(json_config));
   return NVE_SUCCESS;
   C_CATCH
 }

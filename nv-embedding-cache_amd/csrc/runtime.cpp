@@ -4,9 +4,11 @@
 #include "kernels/cache_launch.hpp"
 
 #include <algorithm>
+#include <cctype>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 
 namespace nve_amd {
 
@@ -157,20 +159,182 @@ void ThreadPool::configure_default(int64_t num_workers) {
   g_pool_workers = num_workers;
 }
 
+// ---------------------------------------------------------------------------
+// JSON of the thread-pool configuration (thread_pool.cpp:57-109 parses it with
+// nlohmann::json): the whole text must be one JSON value (RFC 8259), or the
+// call fails as a parse error would; fields are read from a top-level object
+// only (a field of another kind of value is absent).
+// ---------------------------------------------------------------------------
+namespace {
+
+struct JsonReader {
+  const std::string& s;
+  size_t i = 0;
+
+  [[noreturn]] void fail(const char* what) const {
+    throw Error(NVE_ERROR_RUNTIME, cat("Malformed JSON: ", what, " at offset ", i));
+  }
+  void ws() {
+    while (i < s.size() && (s[i] == ' ' || s[i] == '\t' || s[i] == '\n' || s[i] == '\r')) ++i;
+  }
+  bool digit() const { return i < s.size() && s[i] >= '0' && s[i] <= '9'; }
+  std::string string() {  // at the opening quote; returns the decoded text (\u kept as is)
+    ++i;
+    std::string out;
+    while (true) {
+      if (i >= s.size()) fail("unterminated string");
+      const char c = s[i++];
+      if (c == '"') return out;
+      if ((unsigned char)c < 0x20) fail("control character in a string");
+      if (c != '\\') {
+        out += c;
+        continue;
+      }
+      if (i >= s.size()) fail("unterminated escape");
+      const char e = s[i++];
+      switch (e) {
+        case '"': case '\\': case '/': out += e; break;
+        case 'b': out += '\b'; break;
+        case 'f': out += '\f'; break;
+        case 'n': out += '\n'; break;
+        case 'r': out += '\r'; break;
+        case 't': out += '\t'; break;
+        case 'u':
+          for (int k = 0; k < 4; ++k, ++i)
+            if (i >= s.size() || !std::isxdigit((unsigned char)s[i])) fail("bad \\u escape");
+          out += "\\u" + s.substr(i - 4, 4);
+          break;
+        default: fail("bad escape");
+      }
+    }
+  }
+  void number() {
+    if (s[i] == '-') ++i;
+    if (!digit()) fail("bad number");
+    if (s[i] == '0') ++i;
+    else while (digit()) ++i;
+    if (i < s.size() && s[i] == '.') {
+      ++i;
+      if (!digit()) fail("bad fraction");
+      while (digit()) ++i;
+    }
+    if (i < s.size() && (s[i] == 'e' || s[i] == 'E')) {
+      ++i;
+      if (i < s.size() && (s[i] == '+' || s[i] == '-')) ++i;
+      if (!digit()) fail("bad exponent");
+      while (digit()) ++i;
+    }
+  }
+  // one value; with `members`, a top-level object's fields as their raw texts
+  void value(std::map<std::string, std::string>* members = nullptr) {
+    ws();
+    if (i >= s.size()) fail("unexpected end");
+    const char c = s[i];
+    if (c == '{') {
+      ++i;
+      ws();
+      if (i < s.size() && s[i] == '}') {
+        ++i;
+        return;
+      }
+      while (true) {
+        ws();
+        if (i >= s.size() || s[i] != '"') fail("expected a member name");
+        const std::string name = string();
+        ws();
+        if (i >= s.size() || s[i] != ':') fail("expected ':'");
+        ++i;
+        ws();
+        const size_t at = i;
+        value();
+        if (members) (*members)[name] = s.substr(at, i - at);
+        ws();
+        if (i < s.size() && s[i] == ',') {
+          ++i;
+          continue;
+        }
+        if (i < s.size() && s[i] == '}') {
+          ++i;
+          return;
+        }
+        fail("expected ',' or '}'");
+      }
+    }
+    if (c == '[') {
+      ++i;
+      ws();
+      if (i < s.size() && s[i] == ']') {
+        ++i;
+        return;
+      }
+      while (true) {
+        value();
+        ws();
+        if (i < s.size() && s[i] == ',') {
+          ++i;
+          continue;
+        }
+        if (i < s.size() && s[i] == ']') {
+          ++i;
+          return;
+        }
+        fail("expected ',' or ']'");
+      }
+    }
+    if (c == '"') {
+      string();
+      return;
+    }
+    if (c == '-' || (c >= '0' && c <= '9')) {
+      number();
+      return;
+    }
+    for (const char* lit : {"true", "false", "null"}) {
+      const size_t n = std::strlen(lit);
+      if (s.compare(i, n, lit) == 0) {
+        i += n;
+        return;
+      }
+    }
+    fail("unexpected character");
+  }
+};
+
+// The members of the document's top-level object (none when it is another
+// kind of value); throws on malformed JSON.
+std::map<std::string, std::string> json_members(const char* json) {
+  const std::string s(json ? json : "");
+  JsonReader r{s};
+  std::map<std::string, std::string> members;
+  r.ws();
+  const bool object = r.i < s.size() && s[r.i] == '{';
+  r.value(object ? &members : nullptr);
+  r.ws();
+  if (r.i != s.size()) r.fail("trailing characters");
+  return members;
+}
+
+}  // namespace
+
 int64_t json_int_field(const char* json, const char* field, int64_t dflt) {
-  if (json == nullptr) return dflt;
-  const std::string s(json);
-  const std::string q = std::string("\"") + field + "\"";
-  const size_t at = s.find(q);
-  if (at == std::string::npos) return dflt;
-  size_t i = s.find(':', at + q.size());
-  NVE_CHECK_ARG(i != std::string::npos, "Malformed JSON near '", field, "'");
-  ++i;
-  while (i < s.size() && (s[i] == ' ' || s[i] == '\t' || s[i] == '\n')) ++i;
+  const auto m = json_members(json);
+  const auto it = m.find(field);
+  if (it == m.end()) return dflt;
+  const std::string& v = it->second;
   char* end = nullptr;
-  const long long v = std::strtoll(s.c_str() + i, &end, 10);
-  NVE_CHECK_ARG(end != s.c_str() + i, "JSON field '", field, "' must be an integer");
-  return (int64_t)v;
+  const long long x = std::strtoll(v.c_str(), &end, 10);
+  NVE_CHECK_ARG(!v.empty() && end == v.c_str() + v.size(), "JSON field '", field, "' must be an integer");
+  return (int64_t)x;
+}
+
+std::string json_string_field(const char* json, const char* field, const std::string& dflt) {
+  const auto m = json_members(json);
+  const auto it = m.find(field);
+  if (it == m.end()) return dflt;
+  const std::string& v = it->second;
+  NVE_CHECK_ARG(v.size() >= 2 && v.front() == '"', "JSON field '", field, "' must be a string");
+  JsonReader r{v};
+  return r.string();
 }
 
 // ---------------------------------------------------------------------------

@@ -139,8 +139,11 @@ class ThreadPool {
   bool stop_ = false;
 };
 
-// Minimal reader of the thread-pool JSON ({"num_workers": N, ...}).
+// Fields of the thread-pool JSON ({"implementation": "simple", "num_workers": N,
+// ...}): the text must be valid JSON (a parse error is NVE_ERROR_RUNTIME); a
+// field is read from a top-level object, dflt when absent.
 int64_t json_int_field(const char* json, const char* field, int64_t dflt);
+std::string json_string_field(const char* json, const char* field, const std::string& dflt);
 
 // ---------------------------------------------------------------------------
 // execution context: streams, named grow-only scratch buffers, a miss counter
