@@ -44,16 +44,22 @@ struct Entry {
   int64_t logging_interval = -1;
 
   std::mutex mu;                                  // guards the two fields below
-  std::unordered_map<void*, nve_context_t> ctxs;  // lookup stream -> context
+  std::unordered_map<void*, nve_context_t> ctxs;  // lookup stream (or thread) -> context
   int64_t lookups = 0;                            // hit-rate logging counter
 
+  // A context is not thread-safe.  Lookups on a GPU stream share that stream's
+  // context; lookups of CPU keys have no stream, so each calling thread gets a
+  // context of its own, keyed by the address of a thread_local (the reference's
+  // get_cpu_stream, nve_torch_ops_cpu.cpp:22,54), and made with no stream.
   nve_context_t context(void* stream) {
+    static thread_local char thread_key;
+    void* key = stream ? stream : static_cast<void*>(&thread_key);
     std::lock_guard<std::mutex> lk(mu);
-    auto it = ctxs.find(stream);
+    auto it = ctxs.find(key);
     if (it != ctxs.end()) return it->second;
     nve_context_t c = nullptr;
     check(nve_layer_create_execution_context(layer, &c, stream, modify_stream, nullptr, nullptr));
-    ctxs.emplace(stream, c);
+    ctxs.emplace(key, c);
     return c;
   }
 

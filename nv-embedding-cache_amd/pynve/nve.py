@@ -294,15 +294,18 @@ class NVEmbedBinding:
         return self.data_type_
 
     def _ctx(self, stream):
+        # one context per lookup stream; calls with no stream (host work) get
+        # one per calling thread, as a context is not thread-safe
         stream = int(stream or 0)
+        key = stream if stream else ("thread", threading.get_ident())
         with self._ctx_mu:
-            ctx = self._contexts.get(stream)
+            ctx = self._contexts.get(key)
             if ctx is None:
                 h = ctypes.c_void_p()
                 modify = self._modify_stream.cuda_stream if self._modify_stream is not None else 0
                 _lib.call("nve_layer_create_execution_context", self._layer, ctypes.byref(h),
                           ctypes.c_void_p(stream), ctypes.c_void_p(modify), None, None)
-                ctx = self._contexts[stream] = h.value
+                ctx = self._contexts[key] = h.value
             return ctx
 
     def _log_hit_rates(self, hr):

@@ -113,3 +113,105 @@ def test_update_on_a_host_memblock_and_checkpoint_round_trip():
 def test_host_layer_rejects_training():
     with pytest.raises(ValueError):
         nve_layers.NVEmbedding(10, 4, torch.float32, LT.HostLayer, device="cpu")
+
+
+def test_concurrent_gathers_on_one_layer():
+    """test_host_cpu.py:454-497: 8 threads gather disjoint rows of one layer
+    200 times each; row i holds the value i, so a lookup that another thread's
+    scratch clobbered shows at once.  Each calling thread has its own
+    execution context (the module's default row keeps the lookup's hit bits
+    in context scratch)."""
+    import threading
+    rows, dim, nt = 4096, 16, 8
+    w = torch.arange(rows, dtype=torch.float32)[:, None].expand(rows, dim).contiguous()
+    layer = nve_layers.NVEmbedding(rows, dim, torch.float32, LT.HostLayer, weight_init=w,
+                                   optimize_for_training=False, device="cpu")
+    errors = []
+    barrier = threading.Barrier(nt)
+
+    def worker(tid):
+        keys = torch.arange(tid, rows, nt, dtype=torch.int64)
+        want = w[keys]
+        try:
+            barrier.wait()
+            for _ in range(200):
+                if not torch.equal(layer(keys), want):
+                    raise AssertionError(f"thread {tid}: rows of another lookup")
+        except Exception as exc:  # noqa: BLE001 - reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nt)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
+def test_concurrent_gathers_on_distinct_layers():
+    """test_host_cpu.py:500-537: 6 threads, each with its own layer whose
+    values are offset per layer, so a context shared across layers shows."""
+    import threading
+    rows, dim, nt = 1024, 8, 6
+    ws = [(torch.arange(rows, dtype=torch.float32) + t * rows)[:, None].expand(rows, dim).contiguous()
+          for t in range(nt)]
+    layers = [nve_layers.NVEmbedding(rows, dim, torch.float32, LT.HostLayer, weight_init=ws[t],
+                                     optimize_for_training=False, device="cpu") for t in range(nt)]
+    keys = torch.tensor([0, 5, 17, 256, 1023], dtype=torch.int64)
+    errors = []
+    barrier = threading.Barrier(nt)
+
+    def worker(tid):
+        want = ws[tid][keys]
+        try:
+            barrier.wait()
+            for _ in range(200):
+                if not torch.equal(layers[tid](keys), want):
+                    raise AssertionError(f"thread {tid}: another layer's rows")
+        except Exception as exc:  # noqa: BLE001
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nt)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
+def test_binding_lookups_from_several_threads():
+    """The pynve binding itself (nve.HostEmbedding over a caller's memory
+    block, lookups with no stream) from 8 threads: each thread gets its own
+    execution context (a context is not thread-safe).  With a default row the
+    lookup keeps its hit bits in the context's scratch, which threads sharing
+    one context overwrite: rows went missing that way."""
+    import threading
+    rows, dim, nt = 4096, 16, 8
+    table = np.repeat(np.arange(rows, dtype=np.float32)[:, None], dim, axis=1)
+    mb = nve.UserMemBlock(table.ctypes.data, table.nbytes)
+    cfg = nve.EmbedLayerConfig()
+    cfg.default_embedding = [0] * (dim * 4)
+    layer = nve.HostEmbedding(dim, rows, nve.DataType_t.Float32, mb, config=cfg)
+    errors = []
+    barrier = threading.Barrier(nt)
+
+    def worker(tid):
+        keys = np.arange(tid, rows, nt, dtype=np.int64)
+        out = np.zeros((keys.size, dim), np.float32)
+        try:
+            barrier.wait()
+            for _ in range(200):
+                out[:] = -1
+                layer.lookup(keys.size, keys.ctypes.data, out.ctypes.data, 0)
+                if not np.array_equal(out, table[keys]):
+                    raise AssertionError(f"thread {tid}: rows of another lookup")
+        except Exception as exc:  # noqa: BLE001
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nt)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    layer.release_contexts()
