@@ -136,6 +136,44 @@ def test_multi_stream():
     assert nve._native_ops.num_contexts(layer.marker_tensor.data_ptr()) == len(key_sets)
 
 
+@pytest.mark.parametrize("layer_type", [LT.GPULayer, LT.LinearUVM], ids=["gpu", "uvm"])
+def test_multi_thread(layer_type):
+    """test_pytorch.py:711-747: threads share one layer, each lookup on a
+    stream of its own (a 1 MiB cache for the LinearUVM layer, so its default
+    auto-insert runs between lookups); every output equals torch.nn.Embedding."""
+    import threading
+    torch.manual_seed(4)
+    n, nt, iters = 100000, 4, 6
+    ref = torch.nn.Embedding(n, 2, device="cuda")
+    layer = make(layer_type, ref.weight.detach().cpu(), cache=1 << 20)
+    keys = [[torch.randint(0, n, (4096,), device="cuda") for _ in range(iters)] for _ in range(nt)]
+    results = [[] for _ in range(nt)]
+    errors = []
+
+    def worker(t):
+        try:
+            with torch.no_grad():
+                for k in keys[t]:
+                    s = torch.cuda.Stream()
+                    s.wait_stream(torch.cuda.default_stream())
+                    with torch.cuda.stream(s):
+                        results[t].append(layer(k))
+                    s.synchronize()
+        except Exception as exc:  # noqa: BLE001 - reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nt)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    with torch.no_grad():
+        for t in range(nt):
+            for k, out in zip(keys[t], results[t]):
+                assert torch.equal(out, ref(k))
+
+
 def test_multi_layer_registry():
     # test_pytorch.py:433-448
     torch.manual_seed(3)
