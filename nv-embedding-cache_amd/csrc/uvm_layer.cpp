@@ -26,6 +26,9 @@ LinearUVMEmbeddingLayer::LinearUVMEmbeddingLayer(int key_bytes, const LinearUVML
   NVE_CHECK(table_ != nullptr, "Invalid GPU table");
   NVE_CHECK(table_->key_bytes() == key_bytes, "GPU table key type does not match the layer");
   NVE_CHECK(table_->config().uvm_table != nullptr, "LinearUVM layer requires a GPU table with a uvm_table");
+  NVE_CHECK(table_->config().uvm_num_rows > 0, "uvm_num_rows must be >0");
+  NVE_CHECK((uint64_t)table_->config().uvm_num_rows <= (key_bytes == 4 ? (uint64_t)INT32_MAX : (uint64_t)INT64_MAX),
+            "Number of UVM rows cannot be represented by the layer key type");
   NVE_CHECK(cfg_.default_row_index < table_->config().uvm_num_rows,
             "Default row index must be less than the UVM table's row count");
   if (!cfg_.insert_heuristic)
