@@ -255,3 +255,68 @@ def test_quant_pooled(qt, pooling):
     assert np.array_equal(got.view(np.uint16 if nat == O.F16 else np.uint32),
                           ref.view(np.uint16 if nat == O.F16 else np.uint32))
     lay.close()
+
+
+def test_layer_creation_validation():
+    """gpu_layer_test.cpp:371-400,562-581,974-986: an unsupported value type,
+    a NULL table, zero rows, a default row outside the table, more rows than
+    int32 keys can address, and quantized widths without values are refused
+    at creation."""
+    L = _lib.load()
+    buf = torch.zeros(64, dtype=torch.uint8, device="cuda")
+
+    def create(kt=_lib.KEY_INT64, **fields):
+        cfg = L.nve_gpu_embedding_layer_config_default()
+        cfg.layer_name = b"v"
+        cfg.embedding_table = buf.data_ptr()
+        cfg.num_embeddings = 1
+        cfg.embedding_width_in_bytes = 4
+        cfg.value_dtype = _lib.DT_F32
+        for k, v in fields.items():
+            setattr(cfg, k, v)
+        lay = ctypes.c_void_p()
+        st = L.nve_gpu_embedding_layer_create(ctypes.byref(lay), kt, ctypes.byref(cfg), None)
+        if st == _lib.SUCCESS:
+            _lib.call("nve_layer_destroy", lay)
+        return st
+
+    assert create() == _lib.SUCCESS
+    assert create(value_dtype=_lib.DT_F64, embedding_width_in_bytes=8) != _lib.SUCCESS
+    assert create(embedding_table=None) != _lib.SUCCESS
+    assert create(num_embeddings=0) != _lib.SUCCESS
+    assert create(num_embeddings=16, default_row_index=16) != _lib.SUCCESS
+    assert create(_lib.KEY_INT32, num_embeddings=1 << 31) != _lib.SUCCESS
+    assert "cannot be represented" in _lib.last_error()
+    for width in (3, 2, 0):
+        assert create(value_dtype=_lib.DT_QI8_F16, embedding_width_in_bytes=width) != _lib.SUCCESS, width
+
+
+def test_lookup_validation_of_output_and_weight_types():
+    """gpu_layer_test.cpp:583-607 and 987-1010: a float32 table refuses pooled
+    fp16 output and fp16 weights; a quantized table refuses a plain lookup
+    narrower than its rows and Concatenate to Unknown or to the other
+    precision."""
+    rng = np.random.default_rng(5)
+    tb = float_table(rng, 4, 16, O.F32)
+    lay = GpuLayer(tb, _lib.DT_F32)
+    keys = to_dev(np.arange(4, dtype=np.int64))
+    out = torch.zeros((4, 64), dtype=torch.uint8, device="cuda")
+    w = to_dev(np.ones(4, np.float16).view(np.uint16))
+    L = _lib.load()
+    assert L.nve_layer_lookup_pooled(lay.layer, lay.ctx, 4, vp(keys), vp(out), 32, None, _lib.POOL_SUM,
+                                     _lib.SPARSE_FIXED, None, 0, 2, None, 0, _lib.DT_F16, None) == _lib.INVALID_ARGUMENT
+    assert L.nve_layer_lookup_pooled(lay.layer, lay.ctx, 4, vp(keys), vp(out), 64, None, _lib.POOL_WSUM,
+                                     _lib.SPARSE_FIXED, None, 0, 2, vp(w), _lib.DT_F16, _lib.DT_F32,
+                                     None) == _lib.INVALID_ARGUMENT
+    lay.close()
+    qt = quant_table(rng, 4, 16, O.QI8_F32)
+    lay = GpuLayer(qt, _lib.DT_QI8_F32)
+    width = qt.shape[1]
+    assert L.nve_layer_lookup(lay.layer, lay.ctx, 1, vp(keys), vp(out), width - 1, None,
+                              None) == _lib.INVALID_ARGUMENT
+    for odt in (0, _lib.DT_F16):
+        assert L.nve_layer_lookup_pooled(lay.layer, lay.ctx, 1, vp(keys), vp(out), 64, None, _lib.POOL_CONCAT,
+                                         0, None, 0, 0, None, 0, odt, None) == _lib.INVALID_ARGUMENT, odt
+    assert L.nve_layer_lookup_pooled(lay.layer, lay.ctx, 1, vp(keys), vp(out), 64, None, _lib.POOL_CONCAT,
+                                     0, None, 0, 0, None, 0, _lib.DT_F32, None) == _lib.SUCCESS
+    lay.close()
