@@ -24,6 +24,7 @@ layer, the parameter-server tables and the multi-process memory blocks
 """
 import ctypes
 import json
+import sys
 import threading
 from enum import IntEnum
 
@@ -70,6 +71,13 @@ def dtype_size(dtype):
         return _DTYPE_SIZE[DataType_t(dtype)]
     except (KeyError, ValueError):
         raise _lib.InvalidArgument(_lib.INVALID_ARGUMENT, f"dtype {dtype!r} has no element size")
+
+
+def _library_alive():
+    """Whether libnve_amd.so is loaded and still reachable: at interpreter
+    exit the module globals are cleared before the last objects are
+    collected, and their handles are then left to the process's end."""
+    return _lib is not None and getattr(_lib, "_lib", None) is not None
 
 
 class EmbedLayerConfig:
@@ -176,7 +184,9 @@ class _PinnedHost(MemBlock):
                                     f"hipHostMalloc of {size} bytes failed ({rc})")
         super().__init__(kind, p.value or 0, size)
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():
+            return
         if getattr(self, "_ptr", 0) and _hip is not None:
             _hip.hipHostFree(self._ptr)
             self._ptr = 0
@@ -421,7 +431,7 @@ class NVEmbedBinding:
             self._contexts.clear()
 
     def _destroy(self):
-        if getattr(self, "_layer", None) is None or _lib._lib is None:
+        if getattr(self, "_layer", None) is None or not _library_alive():
             return
         try:
             self.release_contexts()
@@ -429,8 +439,11 @@ class NVEmbedBinding:
             _lib._lib.nve_layer_destroy(self._layer)
             self._layer = None
 
-    def __del__(self):
-        self._destroy()
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # at interpreter exit the module's globals may already be gone: the
+        # process's end releases the native handles then
+        if not _finalizing():
+            self._destroy()
 
 
 class GPUEmbedding(NVEmbedBinding):
@@ -529,7 +542,7 @@ class LinearUVMEmbedding(NVEmbedBinding):
         try:
             super()._destroy()
         finally:
-            if getattr(self, "_table", None) is not None and _lib._lib is not None:
+            if getattr(self, "_table", None) is not None and _library_alive():
                 if self._private_stream is not None:
                     self._private_stream.synchronize()
                 _lib._lib.nve_table_destroy(self._table)
@@ -580,7 +593,7 @@ class HostEmbedding(NVEmbedBinding):
         try:
             super()._destroy()
         finally:
-            if getattr(self, "_table", None) is not None and _lib._lib is not None:
+            if getattr(self, "_table", None) is not None and _library_alive():
                 _lib._lib.nve_table_destroy(self._table)
                 self._table = None
 

@@ -19,6 +19,7 @@ storage and the binding.  Layer types:
   Hierarchical  not part of this build (NotImplementedInBuild)
 """
 import builtins
+import sys
 from enum import Enum
 from typing import Optional
 
@@ -267,7 +268,9 @@ class NVEmbeddingBase(torch.nn.Module):
         if HAS_TORCH_OPS:
             nve.register_for_torch(self.marker_tensor.data_ptr(), binding)
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
+        if _finalizing():  # the registry goes with the process
+            return
         marker = getattr(self, "_buffers", {}).get("marker_tensor")
         if HAS_TORCH_OPS and marker is not None:
             nve.unregister_from_torch(marker.data_ptr())

@@ -409,3 +409,20 @@ def test_direct_binding_calls():
         b.lookup_with_pooling(1000, keys.data_ptr(), pooled.data_ptr(),
                               int(nve.PoolingType_t.WeightedSum), 4, off.data_ptr(),
                               int(nve.DataType_t.Float32), wts.data_ptr(), s)
+
+
+@pytest.mark.parametrize("layer_type", [LT.GPULayer, LT.LinearUVM], ids=["gpu", "uvm"])
+def test_distributed_checkpoint_loads_into_the_layer_weight(layer_type, tmp_path):
+    """test_dcp_load.py:112-141 on one process: a torch.distributed.checkpoint
+    of an nn.Embedding's weight loads in place into the layer's weight, and
+    lookups then return the loaded rows."""
+    import torch.distributed.checkpoint as dcp
+    torch.manual_seed(7)
+    ref = torch.nn.Embedding(1000, 8)
+    dcp.save({"embedding": {"embed.weight": ref.weight.detach()}}, checkpoint_id=str(tmp_path))
+    layer = make(layer_type, torch.zeros(1000, 8))
+    dcp.load({"embedding": {"embed.weight": layer.weight}}, checkpoint_id=str(tmp_path))
+    assert torch.equal(layer.weight.detach().cpu(), ref.weight.detach())
+    k = torch.randint(0, 1000, (256,), device="cuda")
+    with torch.no_grad():
+        assert torch.equal(layer(k).cpu(), ref(k.cpu()))

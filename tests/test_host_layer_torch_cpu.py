@@ -215,3 +215,19 @@ def test_binding_lookups_from_several_threads():
         t.join()
     assert not errors, errors
     layer.release_contexts()
+
+
+def test_distributed_checkpoint_loads_into_the_layer_weight(tmp_path):
+    """test_dcp_load.py:112-141 on one process: a torch.distributed.checkpoint
+    of an nn.Embedding's weight is loaded in place into the layer's weight
+    (the table the layer reads), and lookups then return those rows."""
+    import torch.distributed.checkpoint as dcp
+    torch.manual_seed(6)
+    ref = torch.nn.Embedding(10, 2)
+    dcp.save({"embedding": {"embed.weight": ref.weight.detach()}}, checkpoint_id=str(tmp_path))
+    layer = nve_layers.NVEmbedding(10, 2, torch.float32, LT.HostLayer, optimize_for_training=False,
+                                   device="cpu")
+    dcp.load({"embedding": {"embed.weight": layer.weight}}, checkpoint_id=str(tmp_path))
+    assert torch.equal(layer.weight.detach(), ref.weight.detach())
+    k = torch.tensor([1, 5, 9, 0])
+    assert torch.equal(layer(k), ref(k).detach())
