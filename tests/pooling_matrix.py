@@ -12,9 +12,9 @@ rejected, LinearUVM 168 + 112, Host 336 + 0), which the CPU suite checks.
 
 Each enabled case is held to two references: the oracle (bit for bit: the
 same reduction order as the product's kernels, or the HostLayer's CPU order)
-and an independent float64 reduction of the same rows, within the tolerance
-the north star states (1e-5 relative to the bag's magnitude for fp32 output;
-that plus one fp16 ulp for fp16 output)."""
+and an independent float64 reduction of the same rows, within the path's
+pooling tolerance (1e-5 relative to the bag's magnitude for fp32 output; that
+plus one fp16 ulp for fp16 output)."""
 import itertools
 
 import numpy as np
