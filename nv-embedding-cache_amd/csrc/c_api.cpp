@@ -366,7 +366,10 @@ nve_status_t nve_table_insert(nve_table_t table, nve_context_t ctx, int64_t n, c
   NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_insert");
-  if (table->host) return NVE_SUCCESS;  // a linear host table holds every row: no effect
+  if (table->host) {  // a linear host table holds every row: no effect
+    NVE_LOG_INFO("Inserting into linear host table has no effect");
+    return NVE_SUCCESS;
+  }
   table->ptr->insert(*ctx->ptr, n, keys, value_stride, value_size, values);
   return NVE_SUCCESS;
   C_CATCH
@@ -408,7 +411,10 @@ nve_status_t nve_table_clear(nve_table_t table, nve_context_t ctx) {
   NEED_TABLE_CTX
   C_TRY
   NVE_TRACE("nve_table_clear");
-  if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
+  if (table->host) {
+    NVE_LOG_INFO("Clearing linear host table has no effect");
+    return NVE_SUCCESS;
+  }
   table->ptr->clear(*ctx->ptr);
   return NVE_SUCCESS;
   C_CATCH
@@ -419,7 +425,10 @@ nve_status_t nve_table_erase(nve_table_t table, nve_context_t ctx, int64_t n, co
   NEED_KEYS
   C_TRY
   NVE_TRACE("nve_table_erase");
-  if (table->host) return NVE_SUCCESS;  // no effect on a linear host table
+  if (table->host) {
+    NVE_LOG_INFO("Erasing from linear host table has no effect");
+    return NVE_SUCCESS;
+  }
   table->ptr->erase(*ctx->ptr, n, keys);
   return NVE_SUCCESS;
   C_CATCH

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "host_kernels.hpp"
+#include "trace.hpp"
 
 namespace nve_amd {
 
@@ -310,7 +311,8 @@ void HostEmbeddingLayer::pool_gathered(ExecutionContext& ctx, const PoolingParam
 void HostEmbeddingLayer::insert(ExecutionContext&, int64_t, const void*, int64_t, int64_t, const void*,
                                 int64_t table_id) {
   NVE_CHECK(table_id < 1, "Invalid table_id");
-  // a linear host table holds every row already: inserting has no effect
+  // a linear host table holds every row already (linear_host_table.hpp:110-114)
+  NVE_LOG_INFO("Inserting into linear host table has no effect");
 }
 
 void HostEmbeddingLayer::update(ExecutionContext& ctx, int64_t n, const void* keys, int64_t value_stride,
@@ -326,12 +328,15 @@ void HostEmbeddingLayer::accumulate(ExecutionContext& ctx, int64_t n, const void
   table_->update_accumulate(ctx, n, keys, value_stride, value_size, values, value_type);
 }
 
-void HostEmbeddingLayer::clear(ExecutionContext&) {}
+void HostEmbeddingLayer::clear(ExecutionContext&) {
+  NVE_LOG_INFO("Clearing linear host table has no effect");  // linear_host_table.hpp:65-68
+}
 
 void HostEmbeddingLayer::erase(ExecutionContext&, int64_t n, const void* keys, int64_t table_id) {
   NVE_CHECK(table_id < 1, "Invalid table_id");
   if (n < 1) return;
   NVE_CHECK(keys != nullptr, "Invalid keys");
+  NVE_LOG_INFO("Erasing from linear host table has no effect");  // linear_host_table.hpp:72-75
 }
 
 }  // namespace nve_amd

@@ -23,6 +23,7 @@
 #include "host_kernels.hpp"
 #include "kernels/update_launch.hpp"
 #include "layers.hpp"
+#include "trace.hpp"
 
 namespace nve_amd {
 
@@ -178,14 +179,18 @@ void GpuTable::update_accumulate(ExecutionContext& ctx, int64_t n, const void* k
 // ---------------------------------------------------------------------------
 // GPUEmbeddingLayer
 // ---------------------------------------------------------------------------
+// gpu_embedding_layer.cu:500-505,628-640: no effect on a linear table, with a
+// warning that says so
 void GPUEmbeddingLayer::insert(ExecutionContext&, int64_t, const void*, int64_t, int64_t,
                                const void*, int64_t) {
-  // gpu_embedding_layer.cu:500-505: no effect on a linear table (use update)
+  NVE_LOG_WARNING("insert method has no effect for GPU layer, use update to change table content");
 }
 
-void GPUEmbeddingLayer::clear(ExecutionContext&) {}
+void GPUEmbeddingLayer::clear(ExecutionContext&) { NVE_LOG_WARNING("clear method has no effect for GPU layer"); }
 
-void GPUEmbeddingLayer::erase(ExecutionContext&, int64_t, const void*, int64_t) {}
+void GPUEmbeddingLayer::erase(ExecutionContext&, int64_t, const void*, int64_t) {
+  NVE_LOG_WARNING("erase method has no effect for GPU layer");
+}
 
 void GPUEmbeddingLayer::update(ExecutionContext& ctx, int64_t n, const void* keys,
                                int64_t value_stride, int64_t value_size, const void* values,
