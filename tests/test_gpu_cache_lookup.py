@@ -222,3 +222,70 @@ def test_erase_and_clear():
     _lib.call("nve_amd_gpu_table_export_state", ct.table, tags.ctypes.data_as(ctypes.c_void_p), None, None, None)
     assert np.all(tags == -1)
     ct.close()
+
+
+def test_uvm_layer_hit_rates_of_consecutive_lookups_on_every_path():
+    """The LinearUVM layer's hit rate after each of a run of lookups on one
+    context: long pooled bags (the split kernel), short pooled bags and plain
+    lookups, in an order that alternates them, including a batch that all
+    hits and one that all misses: the counter is read and zeroed after each
+    lookup, and every rate equals the oracle's count."""
+    rng = np.random.default_rng(31)
+    rows, dim = 30000, 128
+    uvm = float_table(rng, rows, dim, O.F16, dyadic_values=False)
+    ct = CachedTable(uvm, 2 * 1024 * 1024, 8, value_dtype=_lib.DT_F16)
+    warm(ct, rng, 20000, np.arange(0, 8000), elem_bytes=2)
+    L = _lib.load()
+    never = ctypes.c_void_p()
+    _lib.call("nve_heuristic_create_never", ctypes.byref(never))
+    lc = L.nve_linear_uvm_layer_config_default()
+    lc.insert_heuristic = never.value
+    layer = ctypes.c_void_p()
+    _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), ct.table, None)
+    _lib.call("nve_heuristic_destroy", never)
+    lctx = ctypes.c_void_p()
+    s = stream_ptr()
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
+    tags = ct.model.tags()
+    ways = np.nonzero(tags != -1)[0]
+    resident = tags[ways] * ct.num_sets + ways // 8
+    absent = np.setdiff1d(np.arange(rows), resident)
+    hr = (ctypes.c_float * 1)()
+    kinds = ["long", "long", "short", "long", "plain", "long", "long_all_hit", "long_all_miss", "plain", "long"]
+    for step, kind in enumerate(kinds):
+        bags, hot = (64, 1024) if kind.startswith("long") else (400, 8)
+        n = bags * hot if kind != "plain" else 5000
+        if kind == "long_all_hit":
+            keys = rng.choice(resident, size=n)
+        elif kind == "long_all_miss":
+            keys = rng.choice(absent, size=n)
+        else:
+            keys = np.where(rng.uniform(size=n) < 0.8, rng.integers(0, 8000, size=n),
+                            rng.integers(0, rows, size=n))
+        keys = keys.astype(np.int64)
+        rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+        d_keys = to_dev(keys)
+        if kind == "plain":
+            out = torch.zeros((n, dim), dtype=torch.float16, device="cuda")
+            _lib.call("nve_layer_lookup", layer, lctx, n, vp(d_keys), vp(out), dim * 2, None, hr)
+        else:
+            out = torch.zeros((bags, dim), dtype=torch.float16, device="cuda")
+            _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), dim * 2, None, _lib.POOL_SUM,
+                      _lib.SPARSE_FIXED, None, 0, hot, None, 0, _lib.DT_F16, hr)
+            ref = O.pool(rows_ptr, O.F16, dim, O.FIXED, O.SUM, n, None, bags, hot, None, 0, O.F16)
+            got = out.cpu().numpy().view(np.uint16)
+            if kind == "short":
+                assert np.array_equal(got, ref), step
+            else:  # split bags: fp32 partial sums combined in wave order
+                from nve_helpers import pooled_f16_close
+                assert pooled_f16_close(got, ref), step
+        want = 1.0 - misses / n
+        assert abs(hr[0] - want) < 1e-6, (step, kind, hr[0], want)
+        if kind == "long_all_hit":
+            assert misses == 0
+        if kind == "long_all_miss":
+            assert misses == n
+    _lib.call("nve_context_wait", lctx)
+    _lib.call("nve_context_destroy", lctx)
+    _lib.call("nve_layer_destroy", layer)
+    ct.close()
