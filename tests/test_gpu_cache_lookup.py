@@ -12,7 +12,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from nve_helpers import (csr_offsets, float_table, hip_memcpy, quant_table, stream_ptr, to_dev, vp)
+from nve_helpers import (csr_offsets, float_table, hip_memcpy, pooled_f16_close, quant_table, rel_close,
+                         stream_ptr, to_dev, vp)
 from oracle import oracle as O
 from pynve import _lib
 
@@ -277,7 +278,6 @@ def test_uvm_layer_hit_rates_of_consecutive_lookups_on_every_path():
             if kind == "short":
                 assert np.array_equal(got, ref), step
             else:  # split bags: fp32 partial sums combined in wave order
-                from nve_helpers import pooled_f16_close
                 assert pooled_f16_close(got, ref), step
         want = 1.0 - misses / n
         assert abs(hr[0] - want) < 1e-6, (step, kind, hr[0], want)
@@ -285,6 +285,69 @@ def test_uvm_layer_hit_rates_of_consecutive_lookups_on_every_path():
             assert misses == 0
         if kind == "long_all_miss":
             assert misses == n
+    _lib.call("nve_context_wait", lctx)
+    _lib.call("nve_context_destroy", lctx)
+    _lib.call("nve_layer_destroy", layer)
+    ct.close()
+
+
+@pytest.mark.parametrize("dtype,dim", [(O.F32, 132), (O.F32, 30), (O.F16, 63), (O.F16, 30)])
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_MEAN, _lib.POOL_WSUM, _lib.POOL_WMEAN])
+@pytest.mark.parametrize("bags,hot", [(17, 59), (2048, 5)])
+def test_uvm_layer_pooling_of_odd_row_widths(dtype, dim, pooling, bags, hot):
+    """find_and_combine_lookup_tests.cu's shapes (dims 132, 30 and 63, batches
+    of 17 bags of 59 keys and 2,048 bags) through a cache-backed LinearUVM
+    layer, half the rows resident with negated values so that every hit and
+    miss decision shows: rows whose width is not a multiple of 16 bytes, bit
+    for bit against the oracle's cache model and pooling order."""
+    rng = np.random.default_rng(dim * 7 + pooling * 3 + bags)
+    rows = 6000
+    esz = 4 if dtype == O.F32 else 2
+    uvm = float_table(rng, rows, dim, dtype)
+    ct = CachedTable(uvm, 1 << 20, 8, value_dtype=_lib.DT_F32 if dtype == O.F32 else _lib.DT_F16)
+    warm(ct, rng, 4000, np.arange(0, 3000), elem_bytes=esz)
+    L = _lib.load()
+    never = ctypes.c_void_p()
+    _lib.call("nve_heuristic_create_never", ctypes.byref(never))
+    lc = L.nve_linear_uvm_layer_config_default()
+    lc.insert_heuristic = never.value
+    layer = ctypes.c_void_p()
+    _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), ct.table, None)
+    _lib.call("nve_heuristic_destroy", never)
+    lctx = ctypes.c_void_p()
+    s = stream_ptr()
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
+    n = bags * hot
+    keys = rng.integers(0, rows, size=n).astype(np.int64)
+    weighted = pooling in (_lib.POOL_WSUM, _lib.POOL_WMEAN)
+    w = rng.uniform(0.0, 1.0, size=n).astype(np.float32) if weighted else None
+    rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    out = torch.zeros((bags, dim), dtype=torch.float32 if dtype == O.F32 else torch.float16, device="cuda")
+    hr = (ctypes.c_float * 1)()
+    d_keys = to_dev(keys)
+    d_w = to_dev(w) if weighted else None
+    _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), dim * esz, None, pooling,
+              _lib.SPARSE_FIXED, None, 0, hot, vp(d_w), _lib.DT_F32 if weighted else 0,
+              _lib.DT_F32 if dtype == O.F32 else _lib.DT_F16, hr)
+    torch.cuda.synchronize()
+    ref = O.pool(rows_ptr, dtype, dim, O.FIXED, pooling, n, None, bags, hot, w, O.F32 if weighted else 0, dtype)
+    got = out.cpu().numpy()
+    # 2,048 bags: one lane group per bag, the oracle's key order, bit for bit.
+    # 17 bags: each bag is split over lane groups whose fp32 partial sums are
+    # added in wave order -- exact for the dyadic rows unweighted, within the
+    # pooling tolerance with real weights.
+    exact = bags > 17 or not weighted
+    if dtype == O.F32:
+        if exact:
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        else:
+            assert rel_close(got, ref)
+    else:
+        if exact:
+            assert np.array_equal(got.view(np.uint16), ref)
+        else:
+            assert pooled_f16_close(got.view(np.uint16), ref)
+    assert abs(hr[0] - (1.0 - misses / n)) < 1e-6
     _lib.call("nve_context_wait", lctx)
     _lib.call("nve_context_destroy", lctx)
     _lib.call("nve_layer_destroy", layer)
