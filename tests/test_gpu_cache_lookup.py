@@ -352,3 +352,60 @@ def test_uvm_layer_pooling_of_odd_row_widths(dtype, dim, pooling, bags, hot):
     _lib.call("nve_context_destroy", lctx)
     _lib.call("nve_layer_destroy", layer)
     ct.close()
+
+
+@pytest.mark.parametrize("qt", [O.QI8_F32, O.QU8_F32, O.QI8_F16, O.QU8_F16])
+@pytest.mark.parametrize("count", [132, 30, 63])
+@pytest.mark.parametrize("n", [1000, 4099])
+def test_uvm_layer_dequant_of_odd_row_widths(qt, count, n):
+    """find_and_dequant_tests.cu's shapes (4 quantized formats, 132 / 30 / 63
+    values, 1,000 and 4,099 keys) through a cache-backed LinearUVM layer:
+    Concatenate to the scale's precision, hits from resident rows whose bytes
+    differ from the backing rows, misses over the host link; bit for bit
+    against the oracle's dequantization of the rows the cache model names."""
+    rng = np.random.default_rng(count * 5 + qt + n)
+    rows = 5000
+    q = quant_table(rng, rows, count, qt)
+    # stored rows padded to 4 bytes, as the reference's test lays them out
+    # (find_and_dequant_tests.cu:104-107); the metadata follows the values
+    width = (q.shape[1] + 3) & ~3
+    tb = np.zeros((rows, width), np.uint8)
+    tb[:, :q.shape[1]] = q
+    ct = CachedTable(tb, 1 << 20, 8, value_dtype=qt)
+    warm(ct, rng, 3000, np.arange(0, 2500), elem_bytes=1)
+    L = _lib.load()
+    never = ctypes.c_void_p()
+    _lib.call("nve_heuristic_create_never", ctypes.byref(never))
+    lc = L.nve_linear_uvm_layer_config_default()
+    lc.insert_heuristic = never.value
+    layer = ctypes.c_void_p()
+    _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), ct.table, None)
+    _lib.call("nve_heuristic_destroy", never)
+    lctx = ctypes.c_void_p()
+    s = stream_ptr()
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
+    keys = np.where(rng.uniform(size=n) < 0.7, rng.integers(0, 2500, size=n),
+                    rng.integers(0, rows, size=n)).astype(np.int64)
+    rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    stored = np.stack([np.frombuffer(ctypes.string_at(int(p), width), np.uint8) for p in rows_ptr])
+    nat = O.native_out(qt)
+    oes = 2 if nat == O.F16 else 4
+    out = torch.zeros((n, count * oes), dtype=torch.uint8, device="cuda")
+    hr = (ctypes.c_float * 1)()
+    d_keys = to_dev(keys)
+    _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), count * oes, None, _lib.POOL_CONCAT,
+              0, None, 0, 0, None, 0, nat, hr)
+    torch.cuda.synchronize()
+    ref = O.dequant_rows(stored, qt, count, nat)
+    got = out.cpu().numpy().view(np.uint16 if nat == O.F16 else np.float32).reshape(n, count)
+    assert np.array_equal(got.view(np.uint16 if nat == O.F16 else np.uint32),
+                          ref.view(np.uint16 if nat == O.F16 else np.uint32))
+    assert abs(hr[0] - (1.0 - misses / n)) < 1e-6
+    # the raw rows of the same keys (Concatenate to the stored type is the plain lookup)
+    raw = torch.zeros((n, width), dtype=torch.uint8, device="cuda")
+    _lib.call("nve_layer_lookup", layer, lctx, n, vp(d_keys), vp(raw), width, None, hr)
+    assert np.array_equal(raw.cpu().numpy(), stored)
+    _lib.call("nve_context_wait", lctx)
+    _lib.call("nve_context_destroy", lctx)
+    _lib.call("nve_layer_destroy", layer)
+    ct.close()
