@@ -409,3 +409,57 @@ def test_uvm_layer_dequant_of_odd_row_widths(qt, count, n):
     _lib.call("nve_context_destroy", lctx)
     _lib.call("nve_layer_destroy", layer)
     ct.close()
+
+
+@pytest.mark.parametrize("qt", [O.QI8_F32, O.QU8_F32, O.QI8_F16, O.QU8_F16])
+@pytest.mark.parametrize("count", [132, 30, 63])
+@pytest.mark.parametrize("pooling", [_lib.POOL_SUM, _lib.POOL_WMEAN])
+def test_uvm_layer_quantized_pooling_of_odd_row_widths(qt, count, pooling):
+    """quant_lookup_tests.cu's case through a cache-backed LinearUVM layer:
+    quantized rows of 132 / 30 / 63 values (padded to 4 bytes) pooled over
+    CSR bags of up to 40 keys (one lane group per bag: the oracle's order),
+    hits from resident rows that differ from the backing rows, bit for bit."""
+    rng = np.random.default_rng(count * 11 + qt + pooling)
+    rows, bags = 5000, 300
+    q = quant_table(rng, rows, count, qt)
+    width = (q.shape[1] + 3) & ~3
+    tb = np.zeros((rows, width), np.uint8)
+    tb[:, :q.shape[1]] = q
+    ct = CachedTable(tb, 1 << 20, 8, value_dtype=qt)
+    warm(ct, rng, 3000, np.arange(0, 2500), elem_bytes=1)
+    L = _lib.load()
+    never = ctypes.c_void_p()
+    _lib.call("nve_heuristic_create_never", ctypes.byref(never))
+    lc = L.nve_linear_uvm_layer_config_default()
+    lc.insert_heuristic = never.value
+    layer = ctypes.c_void_p()
+    _lib.call("nve_linear_uvm_layer_create", ctypes.byref(layer), _lib.KEY_INT64, ctypes.byref(lc), ct.table, None)
+    _lib.call("nve_heuristic_destroy", never)
+    lctx = ctypes.c_void_p()
+    s = stream_ptr()
+    _lib.call("nve_layer_create_execution_context", layer, ctypes.byref(lctx), s, s, None, None)
+    off = csr_offsets(rng, bags, 40)
+    n = int(off[-1])
+    keys = np.where(rng.uniform(size=n) < 0.7, rng.integers(0, 2500, size=n),
+                    rng.integers(0, rows, size=n)).astype(np.int64)
+    weighted = pooling == _lib.POOL_WMEAN
+    w = rng.uniform(0.0, 1.0, size=n).astype(np.float32) if weighted else None
+    rows_ptr, _, misses = ct.model.resolve(keys, ct.uvm_np.reshape(-1))
+    nat = O.native_out(qt)
+    oes = 2 if nat == O.F16 else 4
+    out = torch.zeros((bags, count * oes), dtype=torch.uint8, device="cuda")
+    hr = (ctypes.c_float * 1)()
+    d_keys, d_off = to_dev(keys), to_dev(off)
+    d_w = to_dev(w) if weighted else None
+    _lib.call("nve_layer_lookup_pooled", layer, lctx, n, vp(d_keys), vp(out), count * oes, None, pooling,
+              _lib.SPARSE_CSR, vp(d_off), bags + 1, 0, vp(d_w), _lib.DT_F32 if weighted else 0, nat, hr)
+    torch.cuda.synchronize()
+    ref = O.pool(rows_ptr, qt, count, O.CSR, pooling, n, off, bags, 0, w, O.F32 if weighted else 0, nat)
+    got = out.cpu().numpy().view(np.uint16 if nat == O.F16 else np.float32).reshape(bags, count)
+    assert np.array_equal(got.view(np.uint16 if nat == O.F16 else np.uint32),
+                          ref.view(np.uint16 if nat == O.F16 else np.uint32))
+    assert abs(hr[0] - (1.0 - misses / n)) < 1e-6
+    _lib.call("nve_context_wait", lctx)
+    _lib.call("nve_context_destroy", lctx)
+    _lib.call("nve_layer_destroy", layer)
+    ct.close()
